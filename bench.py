@@ -1,0 +1,197 @@
+"""Benchmark: paged decode with an FP8 KV cache on one MI355X.
+
+Workload (default): BASELINE.json configs[2], Llama-3-8B attention shape --
+batch 64, 32 query / 8 KV heads, head_dim 128, OCP e4m3 KV with per-KV-head
+scales (sources bf16 N(0,1) with 1% outliers x8), block_size 16, context
+U{1024..8192}, sequences 0..31 sharing a 1024-token prefix.  A step is one
+decode attention call (one layer) over the whole batch; tokens/s = B / step.
+Two copies of the cache pool alternate between steps so the 256 MB
+Infinity Cache does not hold the previous step's KV.
+
+Prints one JSON line (rank 0).  The CPU baseline is the oracle's
+restatement of the reference CPU path (gather + dequantize + SDPA) on a
+bounded sample of the same workload, timed on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "llm-compileforge_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged-decode tokens/s + HBM GB/s (% peak), Llama-3-8B shape FP8 KV, 1 MI355X"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(case, kc, vc, ks, vs, sample: int, budget_s: float) -> dict:
+    """Times the oracle's CPU restatement on the first `sample` sequences."""
+    import torch
+
+    from oracle.paged_attention import paged_attention_cpu
+
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    idx = list(range(sample))
+    used = sorted({b for i in idx for b in case.block_tables[i]})
+    remap = {b: j for j, b in enumerate(used)}
+    sel = torch.tensor(used, device=kc.device)
+    k_cpu = kc[sel].contiguous().cpu()
+    v_cpu = vc[sel].contiguous().cpu()
+    bt = {f"r{i}": [remap[b] for b in case.block_tables[i]] for i in idx}
+    sl = {f"r{i}": case.seq_lens[i] for i in idx}
+    q = case.q[:sample].float().cpu()
+    kss = ks.cpu() if ks is not None else None
+    vss = vs.cpu() if vs is not None else None
+    paged_attention_cpu(q, k_cpu, v_cpu, bt, sl, case.block_size, case.scale, kss, vss)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        paged_attention_cpu(q, k_cpu, v_cpu, bt, sl, case.block_size, case.scale, kss, vss)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": sample / med,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"first {sample} of {case.batch} sequences of {case.name} "
+        f"({sum(case.seq_lens[:sample])} context tokens), median of {len(times)} runs",
+    }
+
+
+def load_traffic(config: str) -> float | None:
+    path = ROOT / "profiles" / f"traffic_{config}.json"
+    if path.exists():
+        try:
+            return float(json.loads(path.read_text())["hbm_bytes_per_launch"])
+        except (KeyError, ValueError):
+            return None
+    return None
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c3_llama3_8b")
+    ap.add_argument("--batch", type=int, default=None)
+    ap.add_argument("--partition", type=int, default=512)
+    ap.add_argument("--layout", default="native")
+    ap.add_argument("--pools", type=int, default=2, help="cache copies rotated between steps")
+    ap.add_argument("--cpu-sample", type=int, default=8)
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the decode kernel shards per sequence / KV head with no exchange).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from cf_hip import ops, workloads
+
+    dev = torch.device("cuda:0")
+    log(f"device {torch.cuda.get_device_name(dev)}; building {args.config}")
+    case = workloads.make_case(args.config, device=dev, seed=0, batch=args.batch)
+    pools = []
+    for i in range(args.pools):
+        pools.append(workloads.materialize(case, args.layout))
+    tables = case.tables_tensor(dev)
+    lens = case.seq_lens_tensor(dev)
+    plans = [
+        ops.DecodePlan(case.q, kc, vc, tables, lens, case.scale, case.block_size, ks, vs, args.partition)
+        for kc, vc, ks, vs in pools
+    ]
+    ab = workloads.algorithmic_bytes(case)
+    torch.cuda.synchronize()
+    log(f"batch {case.batch}, {ab['tokens']} context tokens, unique bytes {ab['unique'] / 1e6:.1f} MB")
+
+    for i in range(args.warmup):
+        plans[i % len(plans)].run()
+    torch.cuda.synchronize()
+    log("warmup done")
+
+    with ops.KernelTimer() as timer:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            plans[i % len(plans)].run()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    dec_ms, dec_n = timer.query("cf_decode_")
+    red_ms, red_n = timer.query("cf_decode_reduce")
+    main_ms, main_n = dec_ms - red_ms, dec_n - red_n
+    timer.reset()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    log(f"{ms_step * 1e3:.1f} us/step; decode kernel {main_ms / max(main_n, 1) * 1e3:.1f} us, "
+        f"reduce {red_ms / max(red_n, 1) * 1e3:.1f} us")
+
+    avg_main_s = main_ms / max(main_n, 1) / 1e3
+    achieved = ab["unique"] / avg_main_s / 1e9
+    traffic = load_traffic(args.config)
+
+    result = {
+        "metric": METRIC,
+        "value": case.batch / (ms_step / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3 KV / bf16 q / f32 accumulate",
+        "data": "synthetic (seeded), random-init",
+        "config": {
+            "workload": args.config,
+            "batch": case.batch,
+            "num_q_heads": case.q.shape[1],
+            "num_kv_heads": case.num_kv_heads,
+            "head_dim": case.head_dim,
+            "block_size": case.block_size,
+            "context_tokens": ab["tokens"],
+            "partition_tokens": args.partition,
+            "kv_layout": args.layout,
+            "cache_pools_rotated": args.pools,
+            "parallelism": "single GPU",
+        },
+        "hbm_gbs_step": ab["unique"] / (ms_step / 1e3) / 1e9,
+        "hbm_frac_step": ab["unique"] / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS,
+        "kernel_us": {"decode": avg_main_s * 1e6, "reduce": red_ms / max(red_n, 1) * 1e3},
+        "algorithmic_bytes": {"unique": ab["unique"], "logical": ab["logical"]},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+        },
+    }
+    if not args.no_cpu_baseline:
+        kc, vc, ks, vs = pools[0]
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(case, kc, vc, ks, vs, min(args.cpu_sample, case.batch),
+                                              args.cpu_budget)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,162 @@
+/*
+ * cf_hip.h -- C ABI of libcf_hip.so: paged decode attention over a paged
+ * KV cache (bf16 / fp32 / OCP FP8 e4m3) and FP8 KV quantization on MI355X
+ * (gfx950).
+ *
+ * Conventions (all entry points):
+ *   - Return 0 on success and a negative CF_ERR_* code on failure; the
+ *     message is kept per thread and read with cf_last_error().  Nothing is
+ *     thrown across the ABI.
+ *   - Tensors are CfTensor: an SFATensor (include/sfa.h, layout of the
+ *     reference include/sfa.h:54-99) plus a dtype code.  Strides are in
+ *     elements.  Device memory carries device = SFA_ROCM.
+ *   - The caller owns every buffer, including outputs and workspace.  The
+ *     library never frees caller memory and allocates nothing on these
+ *     paths.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the legacy
+ *     default stream) and the calls return without synchronizing.
+ *     Calls are reentrant.
+ *   - Everything a kernel assumes about shapes, dtypes, strides and ranges
+ *     that can be checked on the host is checked before any launch.
+ */
+#ifndef CF_HIP_H
+#define CF_HIP_H
+
+#include <stdint.h>
+
+#include "sfa.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CF_ABI_VERSION 1
+
+/* dtype codes: 0..6 follow the reference's SfaConstant.dtype_code numbering
+ * (reference include/sfa_abi.proto:86); 7 is added for OCP FP8 e4m3fn. */
+typedef enum {
+    CF_F32 = 0,
+    CF_F16 = 1,
+    CF_BF16 = 2,
+    CF_I64 = 3,
+    CF_I32 = 4,
+    CF_I8 = 5,
+    CF_U8 = 6,
+    CF_F8E4M3FN = 7,
+} CfDtype;
+
+typedef struct {
+    SFATensor t;
+    int32_t dtype; /* CfDtype */
+    int32_t reserved;
+} CfTensor;
+
+enum {
+    CF_OK = 0,
+    CF_ERR_INVALID = -1,     /* bad argument: shape, dtype, stride, range  */
+    CF_ERR_HIP = -2,         /* a HIP runtime call failed                  */
+    CF_ERR_WORKSPACE = -3,   /* workspace missing or too small             */
+    CF_ERR_UNSUPPORTED = -4, /* valid request this build does not handle   */
+};
+
+/* ABI version of the loaded library (compare with CF_ABI_VERSION).
+ * Counterpart of the reference's SFA_VERSION (compiler/sfa_abi.py:32-33). */
+int32_t cf_abi_version(void);
+
+/* Copies the calling thread's last error message into buf (NUL-terminated,
+ * truncated to len) and returns the full message length. */
+int32_t cf_last_error(char* buf, uint64_t len);
+
+/* Workspace needed by cf_paged_decode for a batch whose block tables hold at
+ * most max_blocks_per_seq entries.  Replaces no reference function: the
+ * reference decode (kernels/paged_attention.py:21-73) gathers into
+ * temporaries; this path splits long contexts into partitions instead. */
+int32_t cf_paged_decode_workspace_bytes(int64_t batch, int64_t num_q_heads,
+                                        int64_t head_dim,
+                                        int64_t max_blocks_per_seq,
+                                        int32_t block_size,
+                                        int32_t partition_tokens,
+                                        uint64_t* bytes_out);
+
+/* Paged decode attention, one query token per sequence.
+ * Replaces paged_attention / _paged_attention_cpu
+ * (reference kernels/paged_attention.py:200-227, :21-73).
+ *
+ *   q            [B, Hq, D]            f32 | f16 | bf16, D stride 1
+ *   k_cache      [NB, bs, Hkv, D]      f32 | f16 | bf16 | e4m3fn, any strides
+ *   v_cache      [NB, bs, Hkv, D]      same dtype as k_cache, any strides
+ *   block_tables [B, Mb]               i32, physical block ids
+ *   seq_lens     [B]                   i32
+ *   k_scale,     [Hkv] or [1]          f32 dequant scales (e4m3fn caches
+ *   v_scale                            only; NULL otherwise)
+ *   scale        softmax scale (the reference default 1/sqrt(D) is applied
+ *                by the caller)
+ *   out          [B, Hq, D]            dtype of q
+ *
+ * Sequence b attends to its first min(seq_lens[b], Mb*bs) tokens, read
+ * through block_tables[b]; query head h uses KV head h / (Hq/Hkv).
+ * Sequences of length 0 produce zeros.  Block ids must be < NB (not
+ * checked on the device; the Python layer checks host-side tables).
+ * partition_tokens (multiple of bs, >= bs) splits a sequence across
+ * workgroups; the partials are merged by a log-sum-exp reduce. */
+int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache,
+                        const CfTensor* v_cache, const CfTensor* block_tables,
+                        const CfTensor* seq_lens, const CfTensor* k_scale,
+                        const CfTensor* v_scale, float scale,
+                        int32_t block_size, int32_t partition_tokens,
+                        CfTensor* out, void* workspace,
+                        uint64_t workspace_bytes, void* stream);
+
+/* Per-head FP8 scale: scales[h] = amax/448 over x[:, h, :], clamped below
+ * at 1e-12, and 1.0 where amax == 0.  This is
+ * FP8KVCacheQuantizer.quantize_block's scale rule (reference
+ * compiler/quantize/fp8_kv_cache.py:81-86) applied per KV head.
+ *   x       [T, H, Dx]  f32 | f16 | bf16
+ *   scales  [H]         f32 (output) */
+int32_t cf_fp8_amax_scale(const CfTensor* x, CfTensor* scales, void* stream);
+
+/* out[t,h,d] = e4m3fn(f32(x[t,h,d]) / scales[h]) with IEEE division and
+ * round-to-nearest-even, |v| >= 480 -> NaN code (torch's float8_e4m3fn
+ * conversion).  Reference compiler/quantize/fp8_kv_cache.py:89.
+ *   x [T,H,Dx] f32|f16|bf16; scales [H] or [1] f32; out [T,H,Dx] e4m3fn */
+int32_t cf_fp8_quantize(const CfTensor* x, const CfTensor* scales,
+                        CfTensor* out, void* stream);
+
+/* out[t,h,d] = f32(q[t,h,d]) * scales[h].
+ * Reference compiler/quantize/fp8_kv_cache.py:95-105.
+ *   q [T,H,Dx] e4m3fn; scales [H] or [1] f32; out [T,H,Dx] f32 */
+int32_t cf_fp8_dequantize(const CfTensor* q, const CfTensor* scales,
+                          CfTensor* out, void* stream);
+
+/* Writes new K/V rows into a paged e4m3fn cache, quantizing with the given
+ * per-head scales: token i goes to block slot_mapping[i] / bs, offset
+ * slot_mapping[i] % bs (reference token placement:
+ * python_runtime/engine/cache_manager.py:139-171, _kv_cache.py:68-104);
+ * slots < 0 are skipped.
+ *   k_new, v_new  [T, Hkv, D]       f32 | f16 | bf16
+ *   slot_mapping  [T]               i32 | i64
+ *   k_cache,      [NB, bs, Hkv, D]  e4m3fn, any strides
+ *   v_cache
+ *   k_scale,      [Hkv] or [1]      f32
+ *   v_scale
+ * The caller must not target a block that other sequences share. */
+int32_t cf_kv_write_fp8(const CfTensor* k_new, const CfTensor* v_new,
+                        const CfTensor* slot_mapping, CfTensor* k_cache,
+                        CfTensor* v_cache, const CfTensor* k_scale,
+                        const CfTensor* v_scale, void* stream);
+
+/* Kernel timing hook for benchmarks (no reference counterpart).  While
+ * enabled, every kernel this library launches is bracketed by a pair of
+ * HIP events recorded on the launch stream.  cf_profile_query synchronizes
+ * on the recorded events and returns the summed duration (ms) and launch
+ * count of kernels whose name starts with `prefix`. */
+int32_t cf_profile_enable(int32_t on);
+int32_t cf_profile_reset(void);
+int32_t cf_profile_query(const char* prefix, double* total_ms,
+                         int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CF_HIP_H */

@@ -1,0 +1,254 @@
+"""Tensor-level wrappers over the cf_hip C ABI.
+
+Every function here takes ROCm device tensors, enqueues HIP kernels on the
+current torch stream and returns without synchronizing.  There is no CPU
+path: a CPU tensor or a missing libcf_hip.so raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _abi
+from ._abi import check, descriptor, lib, ref, stream_handle
+
+DEFAULT_PARTITION_TOKENS = 512
+
+
+def _require_device(name: str, t: torch.Tensor) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if not t.is_cuda or torch.version.hip is None:
+        raise ValueError(f"{name} must be a ROCm device tensor (got device {t.device})")
+
+
+def _same_device(*ts: torch.Tensor) -> torch.device:
+    dev = ts[0].device
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on {dev}, found one on {t.device}")
+    return dev
+
+
+def decode_workspace_bytes(
+    batch: int, num_q_heads: int, head_dim: int, max_blocks_per_seq: int, block_size: int,
+    partition_tokens: int = DEFAULT_PARTITION_TOKENS,
+) -> int:
+    out = ctypes.c_uint64(0)
+    rc = lib().cf_paged_decode_workspace_bytes(
+        batch, num_q_heads, head_dim, max_blocks_per_seq, block_size, partition_tokens, ctypes.byref(out)
+    )
+    check(rc, "cf_paged_decode_workspace_bytes")
+    return int(out.value)
+
+
+def paged_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    partition_tokens: int = DEFAULT_PARTITION_TOKENS,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Paged decode attention on the GPU; returns out [B, Hq, D] (dtype of q).
+
+    block_tables: int32 [B, Mb]; seq_lens: int32 [B]; caches [NB, bs, Hkv, D]
+    with any strides (f32/f16/bf16/e4m3fn); e4m3fn caches need per-KV-head
+    fp32 k_scale/v_scale of shape [Hkv] or [1].
+    """
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("block_tables", block_tables),
+                    ("seq_lens", seq_lens)):
+        _require_device(name, t)
+    dev = _same_device(q, k_cache, v_cache, block_tables, seq_lens)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=dev)
+    need = decode_workspace_bytes(
+        q.shape[0], q.shape[1], q.shape[2], block_tables.shape[1], block_size, partition_tokens
+    )
+    ws_ptr = None
+    if need > 0:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        ws_ptr = workspace.data_ptr()
+    ks = descriptor(k_scale) if k_scale is not None else None
+    vs = descriptor(v_scale) if v_scale is not None else None
+    dq, dk, dv = descriptor(q), descriptor(k_cache), descriptor(v_cache)
+    dt, dsl, do = descriptor(block_tables), descriptor(seq_lens), descriptor(out)
+    with torch.cuda.device(dev):
+        rc = lib().cf_paged_decode(
+            ref(dq), ref(dk), ref(dv), ref(dt), ref(dsl), ref(ks), ref(vs),
+            float(scale), int(block_size), int(partition_tokens), ref(do),
+            ws_ptr, need, stream_handle(dev),
+        )
+    check(rc, "cf_paged_decode")
+    return out
+
+
+class DecodePlan:
+    """A paged decode call with its descriptors built once.
+
+    For a serving loop that reruns decode over the same buffers (updated in
+    place: q, tables, lengths, cache contents), `run()` costs one C call.
+    The plan keeps references to every tensor it describes.
+    """
+
+    def __init__(
+        self,
+        q: torch.Tensor,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor,
+        block_tables: torch.Tensor,
+        seq_lens: torch.Tensor,
+        scale: float,
+        block_size: int,
+        k_scale: torch.Tensor | None = None,
+        v_scale: torch.Tensor | None = None,
+        partition_tokens: int = DEFAULT_PARTITION_TOKENS,
+        out: torch.Tensor | None = None,
+    ) -> None:
+        for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("block_tables", block_tables),
+                        ("seq_lens", seq_lens)):
+            _require_device(name, t)
+        self.device = _same_device(q, k_cache, v_cache, block_tables, seq_lens)
+        self.out = out if out is not None else torch.empty(q.shape, dtype=q.dtype, device=self.device)
+        self.ws_bytes = decode_workspace_bytes(
+            q.shape[0], q.shape[1], q.shape[2], block_tables.shape[1], block_size, partition_tokens
+        )
+        self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=self.device)
+        self._keep = (q, k_cache, v_cache, block_tables, seq_lens, k_scale, v_scale)
+        self._d = [descriptor(t) for t in (q, k_cache, v_cache, block_tables, seq_lens)]
+        self._ks = descriptor(k_scale) if k_scale is not None else None
+        self._vs = descriptor(v_scale) if v_scale is not None else None
+        self._do = descriptor(self.out)
+        self._args = (
+            *(ref(d) for d in self._d), ref(self._ks), ref(self._vs), float(scale), int(block_size),
+            int(partition_tokens), ref(self._do), self.workspace.data_ptr() if self.ws_bytes else None,
+            self.ws_bytes,
+        )
+        self._fn = lib().cf_paged_decode
+
+    def run(self, stream: int | None = None) -> torch.Tensor:
+        rc = self._fn(*self._args, stream if stream is not None else stream_handle(self.device))
+        check(rc, "cf_paged_decode")
+        return self.out
+
+
+def _as3(x: torch.Tensor) -> torch.Tensor:
+    """Presents x to the C ABI as [T, H, D] or [S0, S1, H, D]: the
+    second-to-last axis is the head axis (the one scales index)."""
+    if x.dim() in (3, 4):
+        return x
+    if x.dim() == 2:
+        return x.unsqueeze(1)
+    if x.dim() < 2:
+        return x.reshape(1, 1, -1)
+    return x.reshape(-1, x.shape[-3], x.shape[-2], x.shape[-1])
+
+
+def fp8_amax_scale(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-head scales [H] = amax(|x[..., h, :]|)/448 (1.0 for all-zero heads, >= 1e-12)."""
+    _require_device("x", x)
+    x3 = _as3(x)
+    if out is None:
+        out = torch.empty(x3.shape[-2], dtype=torch.float32, device=x.device)
+    dx, do = descriptor(x3), descriptor(out)
+    with torch.cuda.device(x.device):
+        rc = lib().cf_fp8_amax_scale(ref(dx), ref(do), stream_handle(x.device))
+    check(rc, "cf_fp8_amax_scale")
+    return out
+
+
+def fp8_quantize(x: torch.Tensor, scales: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """e4m3fn(x / scales[h]); scales has one entry per head (axis -2) or one in total."""
+    _require_device("x", x)
+    _require_device("scales", scales)
+    x3 = _as3(x)
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    o3 = _as3(out)
+    dx, dsc, do = descriptor(x3), descriptor(scales.reshape(-1)), descriptor(o3)
+    with torch.cuda.device(x.device):
+        rc = lib().cf_fp8_quantize(ref(dx), ref(dsc), ref(do), stream_handle(x.device))
+    check(rc, "cf_fp8_quantize")
+    return out
+
+
+def fp8_dequantize(q: torch.Tensor, scales: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """f32(q) * scales[h]."""
+    _require_device("q", q)
+    _require_device("scales", scales)
+    q3 = _as3(q)
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    o3 = _as3(out)
+    dq, dsc, do = descriptor(q3), descriptor(scales.reshape(-1)), descriptor(o3)
+    with torch.cuda.device(q.device):
+        rc = lib().cf_fp8_dequantize(ref(dq), ref(dsc), ref(do), stream_handle(q.device))
+    check(rc, "cf_fp8_dequantize")
+    return out
+
+
+def kv_write_fp8(
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_scale: torch.Tensor,
+    v_scale: torch.Tensor,
+) -> None:
+    """Quantizes new K/V rows [T, Hkv, D] into paged e4m3fn caches at slot_mapping[T]."""
+    for name, t in (("k_new", k_new), ("v_new", v_new), ("slot_mapping", slot_mapping), ("k_cache", k_cache),
+                    ("v_cache", v_cache), ("k_scale", k_scale), ("v_scale", v_scale)):
+        _require_device(name, t)
+    dev = _same_device(k_new, v_new, slot_mapping, k_cache, v_cache, k_scale, v_scale)
+    ds = [descriptor(t) for t in (k_new, v_new, slot_mapping, k_cache, v_cache, k_scale.reshape(-1),
+                                   v_scale.reshape(-1))]
+    with torch.cuda.device(dev):
+        rc = lib().cf_kv_write_fp8(*(ref(d) for d in ds), stream_handle(dev))
+    check(rc, "cf_kv_write_fp8")
+
+
+class KernelTimer:
+    """Sums device time of this library's kernel launches (HIP events)."""
+
+    def __enter__(self) -> "KernelTimer":
+        lib().cf_profile_reset()
+        lib().cf_profile_enable(1)
+        return self
+
+    def __exit__(self, *exc: object) -> None:
+        lib().cf_profile_enable(0)
+
+    @staticmethod
+    def query(prefix: str) -> tuple[float, int]:
+        ms = ctypes.c_double(0.0)
+        n = ctypes.c_int64(0)
+        check(lib().cf_profile_query(prefix.encode(), ctypes.byref(ms), ctypes.byref(n)), "cf_profile_query")
+        return float(ms.value), int(n.value)
+
+    @staticmethod
+    def reset() -> None:
+        lib().cf_profile_reset()
+
+
+__all__ = [
+    "DEFAULT_PARTITION_TOKENS",
+    "DecodePlan",
+    "KernelTimer",
+    "decode_workspace_bytes",
+    "fp8_amax_scale",
+    "fp8_dequantize",
+    "fp8_quantize",
+    "kv_write_fp8",
+    "paged_decode",
+    "_abi",
+]

@@ -1,0 +1,427 @@
+// extern "C" entry points of libcf_hip.so (declared in include/cf_hip.h):
+// argument validation, dispatch to the kernel launchers, error state and
+// the launch-timing hook.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "cf_host.hpp"
+#include "decode_params.hpp"
+#include "kv_fp8.hpp"
+
+namespace cf {
+
+// ---- error state --------------------------------------------------------
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+
+const std::string& last_error() { return g_error; }
+
+int32_t view_of(const CfTensor* t, const char* name, int rank, View* v) {
+  CF_CHECK(t != nullptr, "%s: descriptor is NULL", name);
+  CF_CHECK(t->t.rank == rank, "%s: expected rank %d, got %d", name, rank, t->t.rank);
+  const int eb = dtype_bytes(t->dtype);
+  CF_CHECK(eb > 0, "%s: unknown dtype code %d", name, t->dtype);
+  CF_CHECK(t->t.elem_size == eb, "%s: elem_size %d does not match dtype %s", name, t->t.elem_size,
+           dtype_name(t->dtype));
+  CF_CHECK(t->t.device == SFA_ROCM, "%s: expected device memory (SFA_ROCM), got device %d", name,
+           (int)t->t.device);
+  // The union members share their first three fields; sizes/strides follow.
+  const SFATensorRaw4& r = t->t.r4;
+  const int64_t* sizes = &r.offset + 1;
+  const int64_t* strides = sizes + rank;
+  CF_CHECK(r.offset >= 0, "%s: negative offset", name);
+  v->rank = rank;
+  v->dtype = t->dtype;
+  v->elem = eb;
+  bool empty = false;
+  for (int i = 0; i < rank; ++i) {
+    v->size[i] = sizes[i];
+    v->stride[i] = strides[i];
+    CF_CHECK(sizes[i] >= 0, "%s: negative size on dim %d", name, i);
+    CF_CHECK(strides[i] >= 0, "%s: negative stride on dim %d", name, i);
+    if (sizes[i] == 0) empty = true;
+  }
+  CF_CHECK(empty || r.aligned != nullptr, "%s: NULL data pointer", name);
+  v->base = (char*)r.aligned + r.offset * eb;
+  return CF_OK;
+}
+
+// ---- launch profiling ---------------------------------------------------
+namespace {
+struct ProfRecord {
+  std::string name;
+  hipEvent_t begin, end;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfRecord> g_prof_records;
+std::vector<hipEvent_t> g_prof_pool;
+
+hipEvent_t take_event() {
+  if (!g_prof_pool.empty()) {
+    hipEvent_t e = g_prof_pool.back();
+    g_prof_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+}  // namespace
+
+bool profiling_enabled() { return g_prof_on; }
+
+int profile_begin(const char* name, hipStream_t stream) {
+  if (!g_prof_on) return -1;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  ProfRecord rec{name, take_event(), take_event()};
+  if (!rec.begin || !rec.end) return -1;
+  if (hipEventRecord(rec.begin, stream) != hipSuccess) return -1;
+  g_prof_records.push_back(rec);
+  return (int)g_prof_records.size() - 1;
+}
+
+void profile_end(int slot, hipStream_t stream) {
+  if (slot < 0) return;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  if (slot < (int)g_prof_records.size()) (void)hipEventRecord(g_prof_records[slot].end, stream);
+}
+
+namespace {
+hipStream_t as_stream(void* s) { return (hipStream_t)s; }
+
+// Optional per-head scale vector [H] or [1], f32.
+int32_t scale_view(const CfTensor* t, const char* name, int64_t H, const float** ptr, int64_t* stride) {
+  View v;
+  int32_t rc = view_of(t, name, 1, &v);
+  if (rc) return rc;
+  CF_CHECK(v.dtype == CF_F32, "%s: expected f32, got %s", name, dtype_name(v.dtype));
+  CF_CHECK(v.size[0] == H || v.size[0] == 1, "%s: expected %lld or 1 entries, got %lld", name, (long long)H,
+           (long long)v.size[0]);
+  *ptr = (const float*)v.base;
+  *stride = v.size[0] == 1 ? 0 : v.stride[0];
+  return CF_OK;
+}
+
+bool is_float_dtype(int dt) { return dt == CF_F32 || dt == CF_F16 || dt == CF_BF16; }
+
+// [T, H, D] or [S0, S1, H, D] -> Rank4 (head axis 2).
+Rank4 rank4_of(const View& v) {
+  Rank4 r;
+  r.base = v.base;
+  const int lead = 4 - v.rank;
+  for (int i = 0; i < lead; ++i) {
+    r.size[i] = 1;
+    r.stride[i] = 0;
+  }
+  for (int i = 0; i < v.rank; ++i) {
+    r.size[lead + i] = v.size[i];
+    r.stride[lead + i] = v.stride[i];
+  }
+  return r;
+}
+
+int32_t view_of_34(const CfTensor* t, const char* name, View* v) {
+  CF_CHECK(t != nullptr, "%s: descriptor is NULL", name);
+  CF_CHECK(t->t.rank == 3 || t->t.rank == 4, "%s: expected rank 3 or 4, got %d", name, t->t.rank);
+  return view_of(t, name, t->t.rank, v);
+}
+}  // namespace
+
+}  // namespace cf
+
+using namespace cf;
+
+extern "C" {
+
+int32_t cf_abi_version(void) { return CF_ABI_VERSION; }
+
+int32_t cf_last_error(char* buf, uint64_t len) {
+  const std::string& e = last_error();
+  if (buf && len > 0) {
+    const size_t n = std::min<size_t>(e.size(), (size_t)len - 1);
+    std::memcpy(buf, e.data(), n);
+    buf[n] = '\0';
+  }
+  return (int32_t)e.size();
+}
+
+static int64_t decode_max_parts(int64_t max_blocks, int32_t bs, int32_t pt) {
+  return std::max<int64_t>(1, ceil_div(max_blocks * (int64_t)bs, pt));
+}
+
+int32_t cf_paged_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim,
+                                        int64_t max_blocks_per_seq, int32_t block_size,
+                                        int32_t partition_tokens, uint64_t* bytes_out) {
+  CF_CHECK(bytes_out != nullptr, "bytes_out is NULL");
+  CF_CHECK(batch >= 0 && num_q_heads > 0 && head_dim > 0 && max_blocks_per_seq >= 0,
+           "invalid sizes");
+  CF_CHECK(block_size > 0 && partition_tokens > 0 && partition_tokens % block_size == 0,
+           "partition_tokens (%d) must be a positive multiple of block_size (%d)", partition_tokens,
+           block_size);
+  const int64_t parts = decode_max_parts(max_blocks_per_seq, block_size, partition_tokens);
+  if (parts <= 1) {
+    *bytes_out = 0;
+    return CF_OK;
+  }
+  const uint64_t rows = (uint64_t)batch * num_q_heads * parts;
+  const uint64_t o_bytes = rows * head_dim * 4;
+  const uint64_t ml_bytes = rows * 2 * 4;
+  *bytes_out = ((o_bytes + 255) & ~(uint64_t)255) + ml_bytes;
+  return CF_OK;
+}
+
+int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache, const CfTensor* v_cache,
+                        const CfTensor* block_tables, const CfTensor* seq_lens, const CfTensor* k_scale,
+                        const CfTensor* v_scale, float scale, int32_t block_size, int32_t partition_tokens,
+                        CfTensor* out, void* workspace, uint64_t workspace_bytes, void* stream) {
+  View vq, vk, vv, vt, vs, vo;
+  int32_t rc;
+  if ((rc = view_of(q, "q", 3, &vq))) return rc;
+  if ((rc = view_of(k_cache, "k_cache", 4, &vk))) return rc;
+  if ((rc = view_of(v_cache, "v_cache", 4, &vv))) return rc;
+  if ((rc = view_of(block_tables, "block_tables", 2, &vt))) return rc;
+  if ((rc = view_of(seq_lens, "seq_lens", 1, &vs))) return rc;
+  if ((rc = view_of(out, "out", 3, &vo))) return rc;
+
+  CF_CHECK(is_float_dtype(vq.dtype), "q: dtype must be f32, f16 or bf16, got %s", dtype_name(vq.dtype));
+  CF_CHECK(is_float_dtype(vk.dtype) || vk.dtype == CF_F8E4M3FN,
+           "k_cache: dtype must be f32, f16, bf16 or f8e4m3fn, got %s", dtype_name(vk.dtype));
+  CF_CHECK(vv.dtype == vk.dtype, "v_cache dtype %s differs from k_cache dtype %s", dtype_name(vv.dtype),
+           dtype_name(vk.dtype));
+  CF_CHECK(vt.dtype == CF_I32, "block_tables: expected i32, got %s", dtype_name(vt.dtype));
+  CF_CHECK(vs.dtype == CF_I32, "seq_lens: expected i32, got %s", dtype_name(vs.dtype));
+  CF_CHECK(vo.dtype == vq.dtype, "out dtype %s differs from q dtype %s", dtype_name(vo.dtype),
+           dtype_name(vq.dtype));
+
+  const int64_t B = vq.size[0], Hq = vq.size[1], D = vq.size[2];
+  const int64_t NB = vk.size[0], bs = vk.size[1], Hkv = vk.size[2];
+  for (int i = 0; i < 4; ++i)
+    CF_CHECK(vv.size[i] == vk.size[i], "v_cache shape differs from k_cache shape on dim %d", i);
+  CF_CHECK(vk.size[3] == D, "k_cache head_dim %lld differs from q head_dim %lld", (long long)vk.size[3],
+           (long long)D);
+  CF_CHECK(bs == block_size, "k_cache block dim %lld differs from block_size %d", (long long)bs, block_size);
+  CF_CHECK(Hkv > 0 && Hq % Hkv == 0, "num_heads %lld is not a multiple of num_kv_heads %lld", (long long)Hq,
+           (long long)Hkv);
+  CF_CHECK(D > 0 && D <= 512, "head_dim %lld out of range (1..512)", (long long)D);
+  CF_CHECK(vt.size[0] == B, "block_tables has %lld rows, batch is %lld", (long long)vt.size[0], (long long)B);
+  CF_CHECK(vs.size[0] == B, "seq_lens has %lld entries, batch is %lld", (long long)vs.size[0], (long long)B);
+  CF_CHECK(vo.size[0] == B && vo.size[1] == Hq && vo.size[2] == D, "out shape must be [%lld, %lld, %lld]",
+           (long long)B, (long long)Hq, (long long)D);
+  CF_CHECK(vq.stride[2] == 1 || D == 1, "q: head_dim stride must be 1");
+  CF_CHECK(vo.stride[2] == 1 || D == 1, "out: head_dim stride must be 1");
+  CF_CHECK(block_size > 0, "block_size must be positive");
+  CF_CHECK(partition_tokens > 0 && partition_tokens % block_size == 0,
+           "partition_tokens (%d) must be a positive multiple of block_size (%d)", partition_tokens, block_size);
+  CF_CHECK(NB < (int64_t)INT32_MAX, "too many cache blocks");
+  CF_CHECK(vt.size[1] * (int64_t)bs < (int64_t)INT32_MAX, "block table capacity overflows int32");
+  CF_CHECK(std::isfinite(scale), "scale must be finite");
+
+  DecodeParams p{};
+  p.q = vq.base;
+  p.q_sb = vq.stride[0];
+  p.q_sh = vq.stride[1];
+  p.k = vk.base;
+  p.v = vv.base;
+  for (int i = 0; i < 4; ++i) {
+    p.k_s[i] = vk.stride[i];
+    p.v_s[i] = vv.stride[i];
+  }
+  p.tables = (const int32_t*)vt.base;
+  p.t_sb = vt.stride[0];
+  p.t_sm = vt.stride[1];
+  p.seq_lens = (const int32_t*)vs.base;
+  p.sl_s = vs.stride[0];
+  p.out = vo.base;
+  p.o_sb = vo.stride[0];
+  p.o_sh = vo.stride[1];
+  p.scale = scale;
+  p.B = (int)B;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.G = (int)(Hq / Hkv);
+  p.D = (int)D;
+  p.bs = block_size;
+  p.Mb = (int)vt.size[1];
+  p.PT = partition_tokens;
+  p.max_parts = (int)decode_max_parts(vt.size[1], block_size, partition_tokens);
+
+  if (vk.dtype == CF_F8E4M3FN) {
+    CF_CHECK(k_scale != nullptr && v_scale != nullptr, "f8e4m3fn caches need k_scale and v_scale");
+    if ((rc = scale_view(k_scale, "k_scale", Hkv, &p.k_scale, &p.ks_s))) return rc;
+    if ((rc = scale_view(v_scale, "v_scale", Hkv, &p.v_scale, &p.vs_s))) return rc;
+  } else {
+    CF_CHECK(k_scale == nullptr && v_scale == nullptr, "k_scale/v_scale apply to f8e4m3fn caches only");
+  }
+  if (B == 0) return CF_OK;
+
+  uint64_t need = 0;
+  if ((rc = cf_paged_decode_workspace_bytes(B, Hq, D, vt.size[1], block_size, partition_tokens, &need))) return rc;
+  if (need > 0) {
+    if (workspace == nullptr || workspace_bytes < need) {
+      set_error("workspace of %llu bytes needed, %llu given", (unsigned long long)need,
+                (unsigned long long)workspace_bytes);
+      return CF_ERR_WORKSPACE;
+    }
+    CF_CHECK(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
+    const uint64_t rows = (uint64_t)B * Hq * p.max_parts;
+    p.ws_o = (float*)workspace;
+    p.ws_ml = (float*)((char*)workspace + (((rows * D * 4) + 255) & ~(uint64_t)255));
+  }
+
+  hipStream_t st = as_stream(stream);
+  if (decode_mfma_supported(p, vq.dtype, vk.dtype)) {
+    rc = launch_decode_mfma(p, vq.dtype, vk.dtype, st);
+  } else {
+    rc = launch_decode_generic(p, vq.dtype, vk.dtype, st);
+  }
+  if (rc) return rc;
+  if (p.max_parts > 1) rc = launch_decode_reduce(p, vq.dtype, st);
+  return rc;
+}
+
+int32_t cf_fp8_amax_scale(const CfTensor* x, CfTensor* scales, void* stream) {
+  View vx, vsc;
+  int32_t rc;
+  if ((rc = view_of_34(x, "x", &vx))) return rc;
+  if ((rc = view_of(scales, "scales", 1, &vsc))) return rc;
+  CF_CHECK(is_float_dtype(vx.dtype), "x: dtype must be f32, f16 or bf16, got %s", dtype_name(vx.dtype));
+  CF_CHECK(vsc.dtype == CF_F32, "scales: expected f32, got %s", dtype_name(vsc.dtype));
+  const Rank4 x4 = rank4_of(vx);
+  CF_CHECK(vsc.size[0] == x4.size[2], "scales has %lld entries, x has %lld heads", (long long)vsc.size[0],
+           (long long)x4.size[2]);
+  CF_CHECK(vsc.stride[0] == 1 || vsc.size[0] <= 1, "scales must be contiguous");
+  CF_CHECK(x4.size[2] < 65536, "too many heads");
+  CF_CHECK(x4.size[0] * x4.size[1] / std::max<int64_t>(1, 4096 / std::max<int64_t>(1, x4.size[3])) < (int64_t)INT32_MAX,
+           "x too large");
+  if (x4.size[2] == 0) return CF_OK;
+  return launch_amax_scale(x4, vx.dtype, (float*)vsc.base, 1, as_stream(stream));
+}
+
+int32_t cf_fp8_quantize(const CfTensor* x, const CfTensor* scales, CfTensor* out, void* stream) {
+  View vx, vo;
+  int32_t rc;
+  if ((rc = view_of_34(x, "x", &vx))) return rc;
+  if ((rc = view_of_34(out, "out", &vo))) return rc;
+  CF_CHECK(is_float_dtype(vx.dtype), "x: dtype must be f32, f16 or bf16, got %s", dtype_name(vx.dtype));
+  CF_CHECK(vo.dtype == CF_F8E4M3FN, "out: expected f8e4m3fn, got %s", dtype_name(vo.dtype));
+  const Rank4 x4 = rank4_of(vx), o4 = rank4_of(vo);
+  for (int i = 0; i < 4; ++i) CF_CHECK(o4.size[i] == x4.size[i], "out shape differs from x");
+  const float* sp;
+  int64_t ss;
+  if ((rc = scale_view(scales, "scales", x4.size[2], &sp, &ss))) return rc;
+  return launch_quantize(x4, vx.dtype, sp, ss, o4, as_stream(stream));
+}
+
+int32_t cf_fp8_dequantize(const CfTensor* q, const CfTensor* scales, CfTensor* out, void* stream) {
+  View vq, vo;
+  int32_t rc;
+  if ((rc = view_of_34(q, "q", &vq))) return rc;
+  if ((rc = view_of_34(out, "out", &vo))) return rc;
+  CF_CHECK(vq.dtype == CF_F8E4M3FN, "q: expected f8e4m3fn, got %s", dtype_name(vq.dtype));
+  CF_CHECK(vo.dtype == CF_F32, "out: expected f32, got %s", dtype_name(vo.dtype));
+  const Rank4 q4 = rank4_of(vq), o4 = rank4_of(vo);
+  for (int i = 0; i < 4; ++i) CF_CHECK(o4.size[i] == q4.size[i], "out shape differs from q");
+  const float* sp;
+  int64_t ss;
+  if ((rc = scale_view(scales, "scales", q4.size[2], &sp, &ss))) return rc;
+  return launch_dequantize(q4, sp, ss, o4, as_stream(stream));
+}
+
+int32_t cf_kv_write_fp8(const CfTensor* k_new, const CfTensor* v_new, const CfTensor* slot_mapping,
+                        CfTensor* k_cache, CfTensor* v_cache, const CfTensor* k_scale, const CfTensor* v_scale,
+                        void* stream) {
+  View vk, vv, vsl, vkc, vvc;
+  int32_t rc;
+  if ((rc = view_of(k_new, "k_new", 3, &vk))) return rc;
+  if ((rc = view_of(v_new, "v_new", 3, &vv))) return rc;
+  if ((rc = view_of(slot_mapping, "slot_mapping", 1, &vsl))) return rc;
+  if ((rc = view_of(k_cache, "k_cache", 4, &vkc))) return rc;
+  if ((rc = view_of(v_cache, "v_cache", 4, &vvc))) return rc;
+  CF_CHECK(is_float_dtype(vk.dtype), "k_new: dtype must be f32, f16 or bf16, got %s", dtype_name(vk.dtype));
+  CF_CHECK(vv.dtype == vk.dtype, "v_new dtype differs from k_new dtype");
+  CF_CHECK(vsl.dtype == CF_I32 || vsl.dtype == CF_I64, "slot_mapping: expected i32 or i64, got %s",
+           dtype_name(vsl.dtype));
+  CF_CHECK(vkc.dtype == CF_F8E4M3FN && vvc.dtype == CF_F8E4M3FN, "caches must be f8e4m3fn");
+  for (int i = 0; i < 3; ++i) CF_CHECK(vv.size[i] == vk.size[i], "v_new shape differs from k_new on dim %d", i);
+  for (int i = 0; i < 4; ++i) CF_CHECK(vvc.size[i] == vkc.size[i], "v_cache shape differs from k_cache on dim %d", i);
+  const int64_t T = vk.size[0], H = vk.size[1], D = vk.size[2];
+  CF_CHECK(vsl.size[0] == T, "slot_mapping has %lld entries, %lld tokens given", (long long)vsl.size[0],
+           (long long)T);
+  CF_CHECK(vkc.size[2] == H && vkc.size[3] == D, "cache [NB, bs, %lld, %lld] does not match new rows [T, %lld, %lld]",
+           (long long)vkc.size[2], (long long)vkc.size[3], (long long)H, (long long)D);
+  CF_CHECK(vkc.size[1] > 0, "cache block size must be positive");
+  CF_CHECK(T < (int64_t)INT32_MAX && H * D < (int64_t)INT32_MAX, "too many rows");
+  KvWriteParams p{};
+  if ((rc = scale_view(k_scale, "k_scale", H, &p.k_scale, &p.ks_s))) return rc;
+  if ((rc = scale_view(v_scale, "v_scale", H, &p.v_scale, &p.vs_s))) return rc;
+  p.k_new = rank4_of(vk);
+  p.v_new = rank4_of(vv);
+  p.slots = vsl.base;
+  p.slot_stride = vsl.stride[0];
+  p.k_cache = vkc.base;
+  p.v_cache = vvc.base;
+  for (int i = 0; i < 4; ++i) {
+    p.kc_s[i] = vkc.stride[i];
+    p.vc_s[i] = vvc.stride[i];
+  }
+  p.T = T;
+  p.H = (int)H;
+  p.D = (int)D;
+  p.bs = (int)vkc.size[1];
+  return launch_kv_write_fp8(p, vk.dtype, vsl.dtype, as_stream(stream));
+}
+
+int32_t cf_profile_enable(int32_t on) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  g_prof_on = on != 0;
+  return CF_OK;
+}
+
+int32_t cf_profile_reset(void) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  for (auto& r : g_prof_records) {
+    (void)hipEventSynchronize(r.end);
+    g_prof_pool.push_back(r.begin);
+    g_prof_pool.push_back(r.end);
+  }
+  g_prof_records.clear();
+  return CF_OK;
+}
+
+int32_t cf_profile_query(const char* prefix, double* total_ms, int64_t* launches) {
+  CF_CHECK(prefix != nullptr && total_ms != nullptr && launches != nullptr, "NULL argument");
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  double sum = 0.0;
+  int64_t n = 0;
+  const size_t plen = std::strlen(prefix);
+  for (auto& r : g_prof_records) {
+    if (r.name.compare(0, plen, prefix) != 0) continue;
+    CF_HIP_CHECK(hipEventSynchronize(r.end));
+    float ms = 0.0f;
+    CF_HIP_CHECK(hipEventElapsedTime(&ms, r.begin, r.end));
+    sum += ms;
+    ++n;
+  }
+  *total_ms = sum;
+  *launches = n;
+  return CF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,117 @@
+// Device-side scalar helpers shared by the cf_hip kernels (gfx950).
+//
+// Number formats:
+//   - OCP FP8 E4M3 "fn" (bias 7, no infinities, S.1111.111 is NaN, max 448).
+//     Encoding follows the OCP 8-bit floating point specification (v1.0)
+//     with round-to-nearest-even, and matches torch's float8_e4m3fn cast,
+//     which the reference uses (compiler/quantize/fp8_kv_cache.py:89):
+//     magnitudes >= 480 (and the round-up band (464, 480)) give the NaN code
+//     0x7F, not a saturated 448.
+//   - bfloat16 with round-to-nearest-even and quiet-NaN 0x7FC0, as torch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cf {
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// fp32 -> OCP e4m3fn code, round-to-nearest-even.
+__device__ __forceinline__ uint8_t e4m3_from_f32(float f) {
+  const uint32_t bits = f2u(f);
+  const uint32_t sign = bits & 0x80000000u;
+  const uint32_t mag = bits ^ sign;
+  uint32_t code;
+  if (mag >= 0x43F00000u) {
+    // |f| >= 480, +-inf and NaN all map to the NaN code.
+    code = 0x7Fu;
+  } else if (mag < 0x3C800000u) {
+    // |f| < 2^-6: subnormal range, quantum 2^-9.  |f| * 512 is exact
+    // (power-of-two scaling of a value far from overflow); rint is RNE.
+    code = (uint32_t)__builtin_rintf(u2f(mag) * 512.0f);
+  } else {
+    // Normal range: keep 3 mantissa bits with RNE on the 20 dropped bits,
+    // then rebias the exponent from 127 to 7 (120 << 3 in code units).
+    // A carry out of the mantissa correctly bumps the exponent; values in
+    // (464, 480) round up into the NaN code 0x7F, as the format requires.
+    const uint32_t rounded = mag + 0x7FFFFu + ((mag >> 20) & 1u);
+    code = (rounded >> 20) - (120u << 3);
+  }
+  return (uint8_t)(code | (sign >> 24));
+}
+
+// OCP e4m3fn code -> fp32 (exact).
+__device__ __forceinline__ float f32_from_e4m3(uint32_t c) {
+  const uint32_t sign = (c & 0x80u) << 24;
+  const uint32_t e = (c >> 3) & 0xFu;
+  const uint32_t m = c & 0x7u;
+  uint32_t mag;
+  if (e == 0) {
+    // m * 2^-9, exact in fp32.
+    mag = f2u((float)m * 0.001953125f);
+  } else if (e == 15 && m == 7) {
+    mag = 0x7FC00000u;
+  } else {
+    mag = ((e + 120u) << 23) | (m << 20);
+  }
+  return u2f(sign | mag);
+}
+
+// bf16 <-> fp32
+__device__ __forceinline__ float f32_from_bf16_bits(uint32_t h) { return u2f(h << 16); }
+
+__device__ __forceinline__ uint16_t bf16_bits_from_f32(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Element access by dtype code (CfDtype numbering).
+enum : int { kF32 = 0, kF16 = 1, kBF16 = 2, kI64 = 3, kI32 = 4, kE4M3 = 7 };
+
+template <int DT> struct Elem;
+template <> struct Elem<kF32> {
+  using T = float;
+  static __device__ __forceinline__ float load(const T* p) { return *p; }
+  static __device__ __forceinline__ void store(T* p, float v) { *p = v; }
+};
+template <> struct Elem<kF16> {
+  using T = _Float16;
+  static __device__ __forceinline__ float load(const T* p) { return (float)*p; }
+  static __device__ __forceinline__ void store(T* p, float v) { *p = (_Float16)v; }
+};
+template <> struct Elem<kBF16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(const T* p) { return f32_from_bf16_bits(*p); }
+  static __device__ __forceinline__ void store(T* p, float v) { *p = bf16_bits_from_f32(v); }
+};
+template <> struct Elem<kE4M3> {
+  using T = uint8_t;
+  static __device__ __forceinline__ float load(const T* p) { return f32_from_e4m3(*p); }
+  static __device__ __forceinline__ void store(T* p, float v) { *p = e4m3_from_f32(v); }
+};
+
+// Wavefront (64-lane) reductions.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t w = (uint32_t)__shfl_xor((int)v, o, 64);
+    v = v > w ? v : w;
+  }
+  return v;
+}
+
+}  // namespace cf

@@ -1,0 +1,38 @@
+// Parameters shared by the paged-decode kernels and their host launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cf {
+
+// All strides are in elements of the tensor they index.
+struct DecodeParams {
+  const void* q;
+  int64_t q_sb, q_sh;  // q [B, Hq, D], D stride 1
+  const void* k;
+  const void* v;
+  int64_t k_s[4];  // k_cache [NB, bs, Hkv, D]
+  int64_t v_s[4];  // v_cache [NB, bs, Hkv, D]
+  const int32_t* tables;
+  int64_t t_sb, t_sm;  // block_tables [B, Mb]
+  const int32_t* seq_lens;
+  int64_t sl_s;  // seq_lens [B]
+  const float* k_scale;
+  const float* v_scale;
+  int64_t ks_s, vs_s;  // 0 when the scale is a single value
+  void* out;
+  int64_t o_sb, o_sh;  // out [B, Hq, D], D stride 1
+  float* ws_o;         // [B, Hq, max_parts, D] un-normalized partial outputs
+  float* ws_ml;        // [B, Hq, max_parts, 2] running max and sum
+  float scale;
+  int B, Hq, Hkv, G, D, bs, Mb, PT, max_parts;
+};
+
+// Launchers (return a CF_* status; kernels are enqueued on `stream`).
+int32_t launch_decode_generic(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream);
+int32_t launch_decode_mfma(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream);
+bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt);
+int32_t launch_decode_reduce(const DecodeParams& p, int q_dt, hipStream_t stream);
+
+}  // namespace cf

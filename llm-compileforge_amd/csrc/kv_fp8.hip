@@ -1,0 +1,225 @@
+// FP8 (OCP e4m3fn) KV quantization kernels.
+//
+// Arithmetic follows FP8KVCacheQuantizer (reference
+// compiler/quantize/fp8_kv_cache.py:66-105), applied per KV head:
+//   amax  = max |x|                                  (:81)
+//   scale = 1.0 if amax == 0 else max(amax / 448, 1e-12)   (:82-86)
+//   code  = e4m3fn(f32(x) / scale)                   (:89)
+//   deq   = f32(code) * scale                        (:105)
+// The division is IEEE correctly rounded (the library is built without
+// fast-math and with correctly-rounded fp32 division), so codes and scales
+// are bit-identical to the CPU path.
+#include "cf_device.hpp"
+#include "cf_host.hpp"
+#include "kv_fp8.hpp"
+
+#include <algorithm>
+
+namespace cf {
+
+namespace {
+
+// ---- amax -> scale ------------------------------------------------------
+
+__global__ void zero_u32_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// One workgroup per (row chunk, head).  |x| is compared as unsigned bits:
+// for non-negative floats (and NaN, whose bits exceed +inf) integer order is
+// float order, so atomicMax on the bits gives amax and propagates NaN like
+// torch's max.
+template <int XT>
+__global__ __launch_bounds__(256) void amax_kernel(Rank4 x, uint32_t* amax_bits, int rows_per_block) {
+  const int h = blockIdx.y;
+  const int64_t nrows = x.size[0] * x.size[1];
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < nrows ? r0 + rows_per_block : nrows;
+  using XE = Elem<XT>;
+  const typename XE::T* base = (const typename XE::T*)x.base;
+  uint32_t m = 0;
+  const int64_t D = x.size[3];
+  const int64_t n = (r1 - r0) * D;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const int64_t r = r0 + i / D, d = i % D;
+    const int64_t a = r / x.size[1], t = r % x.size[1];
+    const float v = XE::load(base + a * x.stride[0] + t * x.stride[1] + h * x.stride[2] + d * x.stride[3]);
+    const uint32_t u = f2u(v) & 0x7FFFFFFFu;
+    m = m > u ? m : u;
+  }
+  m = wave_umax(m);
+  if ((threadIdx.x & 63) == 0 && m != 0u) atomicMax(amax_bits + h, m);
+}
+
+__global__ void scale_from_amax_kernel(uint32_t* scale_bits, int64_t stride, int H) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= H) return;
+  uint32_t* slot = scale_bits + h * stride;
+  const float amax = u2f(*slot);
+  float s;
+  if (amax == 0.0f) {
+    s = 1.0f;
+  } else {
+    s = amax / 448.0f;
+    // torch.clamp(min=1e-12): NaN stays NaN, values below the bound are raised.
+    if (s < 1e-12f) s = 1e-12f;
+  }
+  *slot = f2u(s);
+}
+
+// ---- quantize / dequantize ----------------------------------------------
+
+// Flat index -> (a, t, h, d) of a [S0, S1, H, D] view.
+__device__ __forceinline__ int64_t offset4(const Rank4& v, int64_t i) {
+  const int64_t D = v.size[3], H = v.size[2], S1 = v.size[1];
+  const int64_t d = i % D;
+  i /= D;
+  const int64_t h = i % H;
+  i /= H;
+  const int64_t t = i % S1;
+  const int64_t a = i / S1;
+  return a * v.stride[0] + t * v.stride[1] + h * v.stride[2] + d * v.stride[3];
+}
+
+__device__ __forceinline__ int64_t head_of(const Rank4& v, int64_t i) { return (i / v.size[3]) % v.size[2]; }
+
+template <int XT>
+__global__ __launch_bounds__(256) void quantize_kernel(Rank4 x, const float* scales, int64_t s_stride, Rank4 out) {
+  const int64_t n = x.size[0] * x.size[1] * x.size[2] * x.size[3];
+  using XE = Elem<XT>;
+  const typename XE::T* xb = (const typename XE::T*)x.base;
+  uint8_t* ob = (uint8_t*)out.base;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = XE::load(xb + offset4(x, i));
+    ob[offset4(out, i)] = e4m3_from_f32(v / scales[head_of(x, i) * s_stride]);
+  }
+}
+
+__global__ __launch_bounds__(256) void dequantize_kernel(Rank4 q, const float* scales, int64_t s_stride, Rank4 out) {
+  const int64_t n = q.size[0] * q.size[1] * q.size[2] * q.size[3];
+  const uint8_t* qb = (const uint8_t*)q.base;
+  float* ob = (float*)out.base;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    ob[offset4(out, i)] = f32_from_e4m3(qb[offset4(q, i)]) * scales[head_of(q, i) * s_stride];
+  }
+}
+
+// ---- paged KV write -------------------------------------------------------
+
+// One workgroup per new token; threads cover (kv head, d) for K then V.
+template <int XT, int ST>
+__global__ __launch_bounds__(256) void kv_write_kernel(KvWriteParams p) {
+  const int64_t i = blockIdx.x;
+  int64_t slot;
+  if (ST == kI64) slot = ((const int64_t*)p.slots)[i * p.slot_stride];
+  else slot = ((const int32_t*)p.slots)[i * p.slot_stride];
+  if (slot < 0) return;
+  const int64_t blk = slot / p.bs, off = slot % p.bs;
+  using XE = Elem<XT>;
+  const int n = p.H * p.D;
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    const int h = j / p.D, d = j % p.D;
+    const float kv = XE::load((const typename XE::T*)p.k_new.base + i * p.k_new.stride[1] +
+                              h * p.k_new.stride[2] + d * p.k_new.stride[3]);
+    const float vv = XE::load((const typename XE::T*)p.v_new.base + i * p.v_new.stride[1] +
+                              h * p.v_new.stride[2] + d * p.v_new.stride[3]);
+    uint8_t* kd = (uint8_t*)p.k_cache + blk * p.kc_s[0] + off * p.kc_s[1] + h * p.kc_s[2] + d * p.kc_s[3];
+    uint8_t* vd = (uint8_t*)p.v_cache + blk * p.vc_s[0] + off * p.vc_s[1] + h * p.vc_s[2] + d * p.vc_s[3];
+    *kd = e4m3_from_f32(kv / p.k_scale[h * p.ks_s]);
+    *vd = e4m3_from_f32(vv / p.v_scale[h * p.vs_s]);
+  }
+}
+
+int grid_for(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  return (int)(g < 1 ? 1 : g);
+}
+
+}  // namespace
+
+int32_t launch_amax_scale(const Rank4& x, int x_dt, float* scales, int64_t s_stride, hipStream_t stream) {
+  const int H = (int)x.size[2];
+  // The (contiguous) scale vector doubles as the amax accumulator: its fp32
+  // slots hold amax bits until the finalize step turns them into scales.
+  uint32_t* acc = (uint32_t*)scales;
+  {
+    ProfileScope prof("cf_fp8_zero", stream);
+    hipLaunchKernelGGL(zero_u32_kernel, dim3((H + 255) / 256), dim3(256), 0, stream, acc, H);
+  }
+  CF_HIP_CHECK(hipGetLastError());
+  const int64_t T = x.size[0] * x.size[1];
+  if (T > 0 && x.size[3] > 0) {
+    const int rows = (int)std::max<int64_t>(1, 4096 / std::max<int64_t>(1, x.size[3]));
+    const dim3 grid((unsigned)ceil_div(T, rows), H);
+    ProfileScope prof("cf_fp8_amax", stream);
+    switch (x_dt) {
+      case kF32: hipLaunchKernelGGL((amax_kernel<kF32>), grid, dim3(256), 0, stream, x, acc, rows); break;
+      case kF16: hipLaunchKernelGGL((amax_kernel<kF16>), grid, dim3(256), 0, stream, x, acc, rows); break;
+      case kBF16: hipLaunchKernelGGL((amax_kernel<kBF16>), grid, dim3(256), 0, stream, x, acc, rows); break;
+      default: set_error("amax: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
+    }
+    CF_HIP_CHECK(hipGetLastError());
+  }
+  {
+    ProfileScope prof("cf_fp8_scale", stream);
+    hipLaunchKernelGGL(scale_from_amax_kernel, dim3((H + 255) / 256), dim3(256), 0, stream, acc, s_stride, H);
+  }
+  CF_HIP_CHECK(hipGetLastError());
+  return CF_OK;
+}
+
+int32_t launch_quantize(const Rank4& x, int x_dt, const float* scales, int64_t s_stride, const Rank4& out,
+                        hipStream_t stream) {
+  const int64_t n = x.size[0] * x.size[1] * x.size[2] * x.size[3];
+  if (n == 0) return CF_OK;
+  ProfileScope prof("cf_fp8_quantize", stream);
+  const dim3 grid(grid_for(n));
+  switch (x_dt) {
+    case kF32: hipLaunchKernelGGL((quantize_kernel<kF32>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
+    case kF16: hipLaunchKernelGGL((quantize_kernel<kF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
+    case kBF16: hipLaunchKernelGGL((quantize_kernel<kBF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
+    default: set_error("quantize: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
+  }
+  CF_HIP_CHECK(hipGetLastError());
+  return CF_OK;
+}
+
+int32_t launch_dequantize(const Rank4& q, const float* scales, int64_t s_stride, const Rank4& out,
+                          hipStream_t stream) {
+  const int64_t n = q.size[0] * q.size[1] * q.size[2] * q.size[3];
+  if (n == 0) return CF_OK;
+  ProfileScope prof("cf_fp8_dequantize", stream);
+  hipLaunchKernelGGL(dequantize_kernel, dim3(grid_for(n)), dim3(256), 0, stream, q, scales, s_stride, out);
+  CF_HIP_CHECK(hipGetLastError());
+  return CF_OK;
+}
+
+int32_t launch_kv_write_fp8(const KvWriteParams& p, int x_dt, int slot_dt, hipStream_t stream) {
+  if (p.T == 0) return CF_OK;
+  const dim3 grid((unsigned)p.T);
+  const int threads = p.H * p.D >= 256 ? 256 : 64 * (int)ceil_div(p.H * p.D, 64);
+  ProfileScope prof("cf_kv_write_fp8", stream);
+#define CF_KVW(XT, ST) hipLaunchKernelGGL((kv_write_kernel<XT, ST>), grid, dim3(threads), 0, stream, p)
+  if (slot_dt == kI64) {
+    switch (x_dt) {
+      case kF32: CF_KVW(kF32, kI64); break;
+      case kF16: CF_KVW(kF16, kI64); break;
+      case kBF16: CF_KVW(kBF16, kI64); break;
+      default: set_error("kv_write: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
+    }
+  } else {
+    switch (x_dt) {
+      case kF32: CF_KVW(kF32, kI32); break;
+      case kF16: CF_KVW(kF16, kI32); break;
+      case kBF16: CF_KVW(kBF16, kI32); break;
+      default: set_error("kv_write: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
+    }
+  }
+#undef CF_KVW
+  CF_HIP_CHECK(hipGetLastError());
+  return CF_OK;
+}
+
+}  // namespace cf

@@ -1,0 +1,223 @@
+// Paged decode attention: generic VALU kernel (any dtype, any block size,
+// any strides) and the log-sum-exp partition reduce.
+//
+// Semantics follow the reference CPU path (kernels/paged_attention.py:21-73):
+// sequence b attends non-causally to its first min(seq_len, Mb*bs) cached
+// tokens, gathered in block-table order; query head h reads KV head h / G
+// (repeat_interleave, :57-60); softmax(q.k * scale) . v in fp32.
+//
+// Work split: one workgroup per (partition, kv head, sequence).  A
+// partition is PT consecutive tokens.  With more than one partition per
+// sequence the workgroup writes (m, l, o) partials, merged by
+// decode_reduce; with a single partition it writes the output directly.
+#include "cf_device.hpp"
+#include "cf_host.hpp"
+#include "decode_params.hpp"
+
+namespace cf {
+
+namespace {
+
+constexpr int kGenericThreads = 256;
+
+__device__ __forceinline__ int effective_len(const DecodeParams& p, int b) {
+  int ctx = p.seq_lens[(int64_t)b * p.sl_s];
+  const int cap = p.Mb * p.bs;
+  ctx = ctx < cap ? ctx : cap;
+  return ctx > 0 ? ctx : 0;
+}
+
+template <int QT, int KT, bool DIRECT>
+__global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeParams p) {
+  extern __shared__ float smem[];
+  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int G = p.G, D = p.D, bs = p.bs, PT = p.PT;
+  const int ctx = effective_len(p, b);
+  const int start = part * PT;
+
+  using OutE = Elem<QT>;
+  if (start >= ctx) {
+    if (DIRECT && ctx == 0) {
+      for (int i = tid; i < G * D; i += kGenericThreads) {
+        const int g = i / D, d = i % D;
+        OutE::store((typename OutE::T*)p.out + (int64_t)b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d, 0.0f);
+      }
+    }
+    return;
+  }
+  const int count = min(PT, ctx - start);
+
+  float* sq = smem;                           // [G][D]
+  float* sc = sq + G * D;                     // [G][PT]
+  int* sblk = (int*)(sc + G * PT);            // [PT / bs]
+
+  using QE = Elem<QT>;
+  using KE = Elem<KT>;
+  const typename QE::T* qb = (const typename QE::T*)p.q + (int64_t)b * p.q_sb;
+  for (int i = tid; i < G * D; i += kGenericThreads) {
+    const int g = i / D, d = i % D;
+    sq[i] = QE::load(qb + (int64_t)(h * G + g) * p.q_sh + d);
+  }
+  const int nblk = (count + bs - 1) / bs;
+  const int blk0 = start / bs;
+  for (int i = tid; i < nblk; i += kGenericThreads)
+    sblk[i] = p.tables[(int64_t)b * p.t_sb + (int64_t)(blk0 + i) * p.t_sm];
+  __syncthreads();
+
+  const float ks = p.k_scale ? p.k_scale[h * p.ks_s] : 1.0f;
+  const float vs = p.v_scale ? p.v_scale[h * p.vs_s] : 1.0f;
+  const float qk_scale = p.scale * ks;
+
+  // scores
+  const typename KE::T* kbase = (const typename KE::T*)p.k;
+  for (int i = tid; i < count; i += kGenericThreads) {
+    const int tok = start + i;
+    const int64_t blk = sblk[i / bs];
+    const typename KE::T* krow =
+        kbase + blk * p.k_s[0] + (int64_t)(tok % bs) * p.k_s[1] + (int64_t)h * p.k_s[2];
+    for (int g = 0; g < G; ++g) {
+      float acc = 0.0f;
+      const float* qg = sq + g * D;
+      for (int d = 0; d < D; ++d) acc = fmaf(qg[d], KE::load(krow + (int64_t)d * p.k_s[3]), acc);
+      sc[g * PT + i] = acc * qk_scale;
+    }
+  }
+  __syncthreads();
+
+  // softmax statistics per query head: one wave per head
+  const int wave = tid / 64, lane = tid % 64;
+  float* sml = (float*)(sblk + ((PT / bs + 1) & ~1));  // [G][2]
+  for (int g = wave; g < G; g += kGenericThreads / 64) {
+    float m = -INFINITY;
+    for (int i = lane; i < count; i += 64) m = fmaxf(m, sc[g * PT + i]);
+    m = wave_max(m);
+    float l = 0.0f;
+    for (int i = lane; i < count; i += 64) {
+      const float e = expf(sc[g * PT + i] - m);
+      sc[g * PT + i] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      sml[2 * g] = m;
+      sml[2 * g + 1] = l;
+    }
+  }
+  __syncthreads();
+
+  // p . v
+  const typename KE::T* vbase = (const typename KE::T*)p.v;
+  for (int i = tid; i < G * D; i += kGenericThreads) {
+    const int g = i / D, d = i % D;
+    float acc = 0.0f;
+    for (int t = 0; t < count; ++t) {
+      const int tok = start + t;
+      const int64_t blk = sblk[t / bs];
+      const typename KE::T* vrow =
+          vbase + blk * p.v_s[0] + (int64_t)(tok % bs) * p.v_s[1] + (int64_t)h * p.v_s[2];
+      acc = fmaf(sc[g * PT + t], KE::load(vrow + (int64_t)d * p.v_s[3]), acc);
+    }
+    acc *= vs;
+    const int hq = h * G + g;
+    if (DIRECT) {
+      OutE::store((typename OutE::T*)p.out + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d,
+                  acc / sml[2 * g + 1]);
+    } else {
+      const int64_t row = ((int64_t)b * p.Hq + hq) * p.max_parts + part;
+      p.ws_o[row * D + d] = acc;
+      if (d == 0) {
+        p.ws_ml[row * 2] = sml[2 * g];
+        p.ws_ml[row * 2 + 1] = sml[2 * g + 1];
+      }
+    }
+  }
+}
+
+// Merges the partition partials of one (sequence, query head):
+// O = sum_i exp(m_i - M) o_i / sum_i exp(m_i - M) l_i with M = max_i m_i.
+template <int OT>
+__global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
+  const int hq = blockIdx.x, b = blockIdx.y;
+  const int ctx = effective_len(p, b);
+  const int nparts = (ctx + p.PT - 1) / p.PT;
+  using OutE = Elem<OT>;
+  typename OutE::T* o = (typename OutE::T*)p.out + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
+  const int64_t row0 = ((int64_t)b * p.Hq + hq) * p.max_parts;
+  if (nparts == 0) {
+    for (int d = threadIdx.x; d < p.D; d += blockDim.x) OutE::store(o + d, 0.0f);
+    return;
+  }
+  float M = -INFINITY;
+  for (int i = 0; i < nparts; ++i) M = fmaxf(M, p.ws_ml[(row0 + i) * 2]);
+  float L = 0.0f;
+  for (int i = 0; i < nparts; ++i) L += p.ws_ml[(row0 + i) * 2 + 1] * expf(p.ws_ml[(row0 + i) * 2] - M);
+  const float inv = 1.0f / L;
+  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
+    float acc = 0.0f;
+    for (int i = 0; i < nparts; ++i)
+      acc = fmaf(expf(p.ws_ml[(row0 + i) * 2] - M), p.ws_o[(row0 + i) * p.D + d], acc);
+    OutE::store(o + d, acc * inv);
+  }
+}
+
+template <int QT, int KT>
+int32_t launch_generic_t(const DecodeParams& p, hipStream_t stream) {
+  const dim3 grid(p.max_parts, p.Hkv, p.B);
+  const size_t sml_off = (size_t)p.G * p.D + (size_t)p.G * p.PT + (size_t)(((p.PT / p.bs + 1) & ~1));
+  const size_t lds = (sml_off + 2 * (size_t)p.G) * 4;
+  if (lds > 64 * 1024) {
+    set_error("generic decode needs %zu bytes of LDS (G=%d, D=%d, partition=%d); use a smaller partition",
+              lds, p.G, p.D, p.PT);
+    return CF_ERR_UNSUPPORTED;
+  }
+  if (p.max_parts == 1) {
+    ProfileScope prof("cf_decode_generic", stream);
+    hipLaunchKernelGGL((decode_generic_kernel<QT, KT, true>), grid, dim3(kGenericThreads), lds, stream, p);
+  } else {
+    ProfileScope prof("cf_decode_generic", stream);
+    hipLaunchKernelGGL((decode_generic_kernel<QT, KT, false>), grid, dim3(kGenericThreads), lds, stream, p);
+  }
+  CF_HIP_CHECK(hipGetLastError());
+  return CF_OK;
+}
+
+template <int QT>
+int32_t launch_generic_q(const DecodeParams& p, int kv_dt, hipStream_t stream) {
+  switch (kv_dt) {
+    case kF32: return launch_generic_t<QT, kF32>(p, stream);
+    case kF16: return launch_generic_t<QT, kF16>(p, stream);
+    case kBF16: return launch_generic_t<QT, kBF16>(p, stream);
+    case kE4M3: return launch_generic_t<QT, kE4M3>(p, stream);
+  }
+  set_error("unsupported KV dtype %d", kv_dt);
+  return CF_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+
+int32_t launch_decode_generic(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream) {
+  switch (q_dt) {
+    case kF32: return launch_generic_q<kF32>(p, kv_dt, stream);
+    case kF16: return launch_generic_q<kF16>(p, kv_dt, stream);
+    case kBF16: return launch_generic_q<kBF16>(p, kv_dt, stream);
+  }
+  set_error("unsupported q dtype %d", q_dt);
+  return CF_ERR_UNSUPPORTED;
+}
+
+int32_t launch_decode_reduce(const DecodeParams& p, int q_dt, hipStream_t stream) {
+  const dim3 grid(p.Hq, p.B);
+  const int threads = p.D <= 64 ? 64 : (p.D <= 128 ? 128 : 256);
+  ProfileScope prof("cf_decode_reduce", stream);
+  switch (q_dt) {
+    case kF32: hipLaunchKernelGGL((decode_reduce_kernel<kF32>), grid, dim3(threads), 0, stream, p); break;
+    case kF16: hipLaunchKernelGGL((decode_reduce_kernel<kF16>), grid, dim3(threads), 0, stream, p); break;
+    case kBF16: hipLaunchKernelGGL((decode_reduce_kernel<kBF16>), grid, dim3(threads), 0, stream, p); break;
+    default: set_error("unsupported output dtype %d", q_dt); return CF_ERR_UNSUPPORTED;
+  }
+  CF_HIP_CHECK(hipGetLastError());
+  return CF_OK;
+}
+
+}  // namespace cf

@@ -1,0 +1,150 @@
+"""PagedAttention decode over a paged KV cache, on MI355X.
+
+Drop-in for the reference's `kernels/paged_attention.py::paged_attention`
+(reference kernels/paged_attention.py:200-227): same arguments, same
+dict-in/dict-out contract, same edge rules as its CPU path (:21-73).  The
+work runs in libcf_hip.so's HIP kernels; there is no CPU fallback here.
+
+Added, backward-compatible:
+  - keyword-only `k_scale`, `v_scale` (fp32, one per KV head or one in
+    total), required when the caches hold float8_e4m3fn codes;
+  - keyword-only `partition_tokens` (split-KV partition length);
+  - `paged_attention_tensors`, the tensor-native entry the dict API wraps
+    (int32 block tables [B, Mb], int32 lengths [B], output [B, Hq, D]).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from cf_hip import ops as _ops
+
+DEFAULT_PARTITION_TOKENS = _ops.DEFAULT_PARTITION_TOKENS
+
+
+def _require_rocm(q: torch.Tensor) -> None:
+    if not (isinstance(q, torch.Tensor) and q.is_cuda and torch.version.hip is not None):
+        where = q.device if isinstance(q, torch.Tensor) else type(q).__name__
+        raise ValueError(
+            f"paged_attention runs on ROCm device tensors only (got {where}); "
+            "move q, k_cache and v_cache to the GPU"
+        )
+
+
+def paged_attention_tensors(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    block_size: int = 16,
+    scale: float | None = None,
+    *,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    partition_tokens: int = DEFAULT_PARTITION_TOKENS,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Decode attention for a batch held in tensors.
+
+    Args:
+        q: [B, Hq, D] query, one token per sequence.
+        k_cache, v_cache: [num_blocks, block_size, Hkv, D] (any strides).
+        block_tables: int32 [B, Mb] physical block ids per sequence.
+        seq_lens: int32 [B]; sequence b attends to its first
+            min(seq_lens[b], Mb*block_size) tokens (0 gives a zero row).
+        block_size: tokens per block (must equal k_cache.shape[1]).
+        scale: softmax scale, default 1/sqrt(D).
+        k_scale, v_scale: dequant scales for float8_e4m3fn caches.
+
+    Returns:
+        [B, Hq, D] tensor in q's dtype.
+    """
+    _require_rocm(q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    if block_tables.dtype != torch.int32:
+        block_tables = block_tables.to(torch.int32)
+    if seq_lens.dtype != torch.int32:
+        seq_lens = seq_lens.to(torch.int32)
+    return _ops.paged_decode(
+        q, k_cache, v_cache, block_tables, seq_lens, float(scale), int(block_size),
+        k_scale=k_scale, v_scale=v_scale, partition_tokens=partition_tokens, out=out, workspace=workspace,
+    )
+
+
+def paged_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: dict[str, list[int]],
+    seq_lens: dict[str, int],
+    block_size: int = 16,
+    scale: float | None = None,
+    *,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    partition_tokens: int = DEFAULT_PARTITION_TOKENS,
+) -> dict[str, torch.Tensor]:
+    """PagedAttention with block table indirection.
+
+    Args:
+        q:  Query tensor [batch, num_heads, head_dim] (decode: one token per request).
+        k_cache: Paged K cache [num_blocks, block_size, num_kv_heads, head_dim].
+        v_cache: Paged V cache [num_blocks, block_size, num_kv_heads, head_dim].
+        block_tables: request_id -> list[physical block IDs].
+        seq_lens: request_id -> current sequence length.
+        block_size: Tokens per KV block (default 16).
+        scale: Attention scale (default 1/sqrt(head_dim)).
+        k_scale, v_scale: FP8 dequant scales (float8_e4m3fn caches only).
+
+    Returns:
+        dict mapping request_id -> output tensor [num_heads, head_dim].
+
+    Request i of the dict (insertion order) uses q[i]; a request missing
+    from seq_lens attends to len(blocks) * block_size tokens; a length past
+    the table's capacity is cut to it (reference
+    kernels/paged_attention.py:36-48).
+    """
+    _require_rocm(q)
+    rids = list(block_tables.keys())
+    if len(rids) > q.shape[0]:
+        raise IndexError(f"{len(rids)} requests but q holds {q.shape[0]} rows")
+    nb = k_cache.shape[0]
+    lens: list[int] = []
+    tables: list[list[int]] = []
+    for rid in rids:
+        blocks = block_tables[rid]
+        seq_len = seq_lens.get(rid, len(blocks) * block_size)
+        n_blocks = min(len(blocks), (seq_len + block_size - 1) // block_size)
+        if n_blocks <= 0:
+            # The reference fails here too (torch.cat of an empty list).
+            raise RuntimeError(f"request {rid!r}: no KV blocks to attend (seq_len={seq_len})")
+        used = []
+        for bid in blocks[:n_blocks]:
+            bid = int(bid)
+            if not -nb <= bid < nb:
+                raise IndexError(f"request {rid!r}: block id {bid} out of range for {nb} cache blocks")
+            used.append(bid + nb if bid < 0 else bid)
+        tables.append(used)
+        lens.append(min(seq_len, n_blocks * block_size))
+    if not rids:
+        return {}
+    mb = max(len(t) for t in tables)
+    host_tables = torch.zeros(len(rids), mb, dtype=torch.int32, pin_memory=True)
+    for i, t in enumerate(tables):
+        host_tables[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    host_lens = torch.tensor(lens, dtype=torch.int32).pin_memory()
+    dev_tables = host_tables.to(q.device, non_blocking=True)
+    dev_lens = host_lens.to(q.device, non_blocking=True)
+    out = paged_attention_tensors(
+        q[: len(rids)], k_cache, v_cache, dev_tables, dev_lens, block_size, scale,
+        k_scale=k_scale, v_scale=v_scale, partition_tokens=partition_tokens,
+    )
+    return {rid: out[i] for i, rid in enumerate(rids)}
+
+
+__all__ = ["DEFAULT_PARTITION_TOKENS", "paged_attention", "paged_attention_tensors"]

@@ -1,0 +1,112 @@
+"""HIP backend of the HAL: the paged-attention path as OpExecutor ops.
+
+Follows the reference's "registered kernel, else fallback" dispatch
+(python_runtime/hal/triton_backend.py:58-65): ops this backend implements
+run as HIP kernels from libcf_hip.so; any other op goes to the fallback
+executor (for example the reference's PyTorchBackend); with no fallback an
+unknown op raises ValueError("Unknown op: ...") like the reference's
+PyTorchBackend.execute (pytorch_backend/__init__.py:111-113).
+
+Ops:
+  paged_attention     inputs [query, key_cache, value_cache, block_table
+                      (, seq_lens)] -- the operand list of the reference's
+                      planned hal.paged_attention op
+                      (sf-dialect/include/Sf/HALOps.td:184-189).  kwargs:
+                      seq_lens, block_size, scale, k_scale, v_scale,
+                      partition_tokens.  Returns [B, Hq, D].
+  kv_cache_write_fp8  inputs [k_new, v_new, slot_mapping, key_cache,
+                      value_cache, k_scale, v_scale]; returns key_cache.
+  fp8_amax_scale      inputs [x]; per-head scales [H] (head axis -2).
+  fp8_quantize        inputs [x, scales]; e4m3fn codes.
+  fp8_dequantize      inputs [codes, scales]; float32 values.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable
+from typing import Any
+
+import torch
+
+from cf_hip import ops as _ops
+from python_runtime.hal import registry
+from python_runtime.hal.interface import OpExecutor
+
+# op name -> (min inputs, max inputs)
+_ARITY: dict[str, tuple[int, int]] = {
+    "paged_attention": (4, 5),
+    "kv_cache_write_fp8": (7, 7),
+    "fp8_amax_scale": (1, 1),
+    "fp8_quantize": (2, 2),
+    "fp8_dequantize": (2, 2),
+}
+
+
+class HipBackend(OpExecutor):
+    """OpExecutor running the paged-attention path on MI355X.
+
+    Args:
+        fallback: executor for ops this backend does not implement.
+        partition_tokens: default split-KV partition length for decode.
+    """
+
+    def __init__(self, fallback: OpExecutor | None = None, partition_tokens: int = _ops.DEFAULT_PARTITION_TOKENS):
+        self._fallback = fallback
+        self._partition_tokens = partition_tokens
+        self._handlers: dict[str, Callable[..., torch.Tensor]] = {
+            "paged_attention": self._paged_attention,
+            "kv_cache_write_fp8": self._kv_cache_write_fp8,
+            "fp8_amax_scale": lambda inputs, **kw: _ops.fp8_amax_scale(inputs[0]),
+            "fp8_quantize": lambda inputs, **kw: _ops.fp8_quantize(inputs[0], inputs[1]),
+            "fp8_dequantize": lambda inputs, **kw: _ops.fp8_dequantize(inputs[0], inputs[1]),
+        }
+
+    @staticmethod
+    def supported_ops() -> list[str]:
+        return sorted(_ARITY)
+
+    def execute(self, op_name: str, inputs: list[Any], **kwargs: Any) -> torch.Tensor:
+        handler = self._handlers.get(op_name)
+        if handler is None:
+            if self._fallback is not None:
+                return self._fallback.execute(op_name, inputs, **kwargs)
+            raise ValueError(f"Unknown op: {op_name}")
+        lo, hi = _ARITY[op_name]
+        n = len(inputs)
+        if n < lo:
+            raise ValueError(f"Op '{op_name}' requires at least {lo} inputs, got {n}")
+        if n > hi:
+            raise ValueError(f"Op '{op_name}' accepts at most {hi} inputs, got {n}")
+        return handler(inputs, **kwargs)
+
+    def _paged_attention(self, inputs: list[Any], **kw: Any) -> torch.Tensor:
+        from kernels.paged_attention import paged_attention_tensors
+
+        q, k_cache, v_cache, table = inputs[:4]
+        seq_lens = inputs[4] if len(inputs) > 4 else kw.get("seq_lens")
+        block_size = int(kw.get("block_size", k_cache.shape[1]))
+        if seq_lens is None:
+            # The reference default for a request without a length: the whole table.
+            seq_lens = torch.full((table.shape[0],), table.shape[1] * block_size, dtype=torch.int32,
+                                  device=table.device)
+        elif not isinstance(seq_lens, torch.Tensor):
+            seq_lens = torch.tensor(list(seq_lens), dtype=torch.int32, device=table.device)
+        return paged_attention_tensors(
+            q, k_cache, v_cache, table, seq_lens, block_size, kw.get("scale"),
+            k_scale=kw.get("k_scale"), v_scale=kw.get("v_scale"),
+            partition_tokens=int(kw.get("partition_tokens", self._partition_tokens)),
+        )
+
+    def _kv_cache_write_fp8(self, inputs: list[Any], **kw: Any) -> torch.Tensor:
+        k_new, v_new, slots, k_cache, v_cache, k_scale, v_scale = inputs
+        _ops.kv_write_fp8(k_new, v_new, slots, k_cache, v_cache, k_scale, v_scale)
+        return k_cache
+
+
+def register_hip_backend(name: str = "hip") -> None:
+    """Registers HipBackend's factory under `name` (once per process)."""
+    if name not in registry.list_backends():
+        registry.register(name, lambda **kw: HipBackend(**kw))
+
+
+__all__ = ["HipBackend", "register_hip_backend"]

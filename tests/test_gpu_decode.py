@@ -1,0 +1,175 @@
+"""GPU parity of the paged decode kernels against the CPU oracle.
+
+Tolerances: fp32 max-abs 1e-5; bf16 and fp8
+max-abs 2e-2 with cosine >= 0.9999.  Small and mid sizes compare with the
+float64 oracle directly; full benchmark sizes use size-independent
+properties (block-permutation invariance, shared prefix == copied prefix,
+split-KV == no split) plus an oracle check on a sample of sequences.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cf_hip import layout as L
+from cf_hip import ops, workloads
+from kernels.paged_attention import paged_attention, paged_attention_tensors
+from tests.gpu_util import assert_close, metrics, oracle_decode
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(case, kc, vc, ks, vs, dev, pt=512, tables=None, lens=None):
+    t = tables if tables is not None else case.tables_tensor(dev)
+    s = lens if lens is not None else case.seq_lens_tensor(dev)
+    out = paged_attention_tensors(case.q, kc, vc, t, s, case.block_size, case.scale, k_scale=ks, v_scale=vs,
+                                  partition_tokens=pt)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("layout", ["native", "token_major"])
+@pytest.mark.parametrize("config,batch", [("c1_opt125m", None), ("c2_tinyllama", None), ("c3_llama3_8b", 6),
+                                          ("c4_llama3_70b", 3)])
+def test_configs_match_oracle(gpu, config, batch, layout):
+    print(f"[case] {config} batch={batch} layout={layout}", flush=True)
+    case = workloads.make_case(config, device=gpu, seed=21, batch=batch)
+    kc, vc, ks, vs = workloads.materialize(case, layout)
+    out = _run(case, kc, vc, ks, vs, gpu)
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    assert_close(out.float().cpu().numpy(), ref, case.q.dtype, f"{config}/{layout}")
+
+
+@pytest.mark.parametrize("pt", [16, 64, 256, 4096])
+def test_partition_sizes_agree(gpu, pt):
+    print(f"[case] c2 partitions={pt}", flush=True)
+    case = workloads.make_case("c2_tinyllama", device=gpu, seed=3, batch=8)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    out = _run(case, kc, vc, ks, vs, gpu, pt=pt)
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    assert_close(out.float().cpu().numpy(), ref, case.q.dtype, f"pt={pt}")
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [(8, 8, 64, 16), (8, 2, 128, 16), (16, 1, 64, 16), (32, 2, 128, 16),
+                                         (4, 4, 32, 8), (8, 2, 64, 32), (6, 3, 80, 16), (8, 4, 256, 16)])
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
+def test_shapes_and_dtypes(gpu, hq, hkv, d, bs, kv_dtype):
+    print(f"[case] hq={hq} hkv={hkv} d={d} bs={bs} kv={kv_dtype}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(hq * 1000 + d + bs)
+    b, nb = 5, 64
+    lens = [1, bs, bs + 1, 7 * bs - 3, 700]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(1)).tolist()
+    tables, pos = [], 0
+    for n in lens:
+        k = (n + bs - 1) // bs
+        tables.append(perm[pos:pos + k])
+        pos += k
+    q_dtype = torch.float32 if kv_dtype == torch.float32 else torch.bfloat16
+    q = torch.randn(b, hq, d, generator=g, device=gpu).to(q_dtype)
+    ksrc = torch.randn(nb, bs, hkv, d, generator=g, device=gpu).to(q_dtype)
+    vsrc = torch.randn(nb, bs, hkv, d, generator=g, device=gpu).to(q_dtype)
+    case = workloads.DecodeCase("adhoc", q, ksrc, vsrc, tables, lens, bs, 1 / math.sqrt(d), kv_dtype)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    out = _run(case, kc, vc, ks, vs, gpu, pt=4 * bs)
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    assert_close(out.float().cpu().numpy(), ref, q_dtype, f"{hq}/{hkv}/{d}/{bs}/{kv_dtype}")
+
+
+def test_edge_lengths(gpu):
+    """Zero length -> zeros; length past the table -> truncated to it."""
+    case = workloads.make_case("c2_tinyllama", device=gpu, seed=4, batch=4)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    tables = case.tables_tensor(gpu)
+    cap = tables.shape[1] * 16
+    lens = torch.tensor([0, 10**6, 1, 17], dtype=torch.int32, device=gpu)
+    out = _run(case, kc, vc, ks, vs, gpu, tables=tables, lens=lens).float().cpu().numpy()
+    assert np.all(out[0] == 0)
+    eff = [0, cap, 1, 17]
+    ref = oracle_decode(case, kc, vc, ks, vs, tables=tables.cpu().tolist(), lens=eff)
+    assert_close(out[1:], ref[1:], case.q.dtype, "edge lengths")
+
+
+def test_dict_api_matches_tensor_api_and_reference_rules(gpu):
+    case = workloads.make_case("c2_tinyllama", device=gpu, seed=5, batch=6)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    rids = [f"r{i}" for i in range(case.batch)]
+    bt = dict(zip(rids, case.block_tables))
+    sl = {r: n for r, n in zip(rids, case.seq_lens) if r != "r2"}  # r2: whole table
+    sl["r3"] = 10**6  # beyond capacity: truncated
+    out = paged_attention(case.q, kc, vc, bt, sl, block_size=16)
+    assert list(out) == rids
+    lens = [len(t) * 16 if i in (2, 3) else n for i, (t, n) in enumerate(zip(case.block_tables, case.seq_lens))]
+    ref = oracle_decode(case, kc, vc, ks, vs, lens=lens)
+    got = torch.stack([out[r] for r in rids]).float().cpu().numpy()
+    assert_close(got, ref, case.q.dtype, "dict api")
+    with pytest.raises(RuntimeError):
+        paged_attention(case.q, kc, vc, {"x": [0]}, {"x": 0})
+    with pytest.raises(IndexError):
+        paged_attention(case.q, kc, vc, {"x": [kc.shape[0]]}, {"x": 3})
+
+
+def test_full_c3_properties(gpu):
+    """Full headline config: block-permutation invariance (bitwise), shared
+    prefix == copied prefix (bitwise), split-KV sizes agree, and the oracle
+    on a sample of sequences."""
+    print("[case] c3 full size", flush=True)
+    case = workloads.make_case("c3_llama3_8b", device=gpu, seed=0)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    out = _run(case, kc, vc, ks, vs, gpu)
+    # 1. permutation of physical block ids
+    nb = kc.shape[0]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(2)).to(gpu)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(nb, device=gpu)
+    kc2, vc2 = L.alloc_kv_cache(nb, 16, 8, 128, torch.float8_e4m3fn, gpu)
+    kc2.copy_(kc[perm])
+    vc2.copy_(vc[perm])
+    t2 = inv[case.tables_tensor(gpu).long()].to(torch.int32)
+    out2 = _run(case, kc2, vc2, ks, vs, gpu, tables=t2)
+    assert torch.equal(out, out2)
+    del kc2, vc2
+    # 2. copied prefix
+    pre = case.meta["shared_prefix_blocks"]
+    tables = case.tables_tensor(gpu)
+    shared = tables[0, :pre].long()
+    kc3, vc3 = L.alloc_kv_cache(nb + pre, 16, 8, 128, torch.float8_e4m3fn, gpu)
+    kc3[:nb].copy_(kc)
+    vc3[:nb].copy_(vc)
+    kc3[nb:].copy_(kc[shared])
+    vc3[nb:].copy_(vc[shared])
+    t3 = tables.clone()
+    t3[1, :pre] = torch.arange(nb, nb + pre, device=gpu, dtype=torch.int32)
+    out3 = _run(case, kc3, vc3, ks, vs, gpu, tables=t3)
+    assert torch.equal(out, out3)
+    del kc3, vc3
+    # 3. partition sizes
+    for pt in (256, 2048, 8192):
+        o = _run(case, kc, vc, ks, vs, gpu, pt=pt)
+        err, cos = metrics(o.float().cpu().numpy(), out.float().cpu().numpy())
+        assert err < 2e-2 and cos > 0.9999, (pt, err, cos)
+    # 4. oracle on a sample of sequences (shared and private)
+    idx = [0, 1, 31, 32, 63]
+    sub = workloads.DecodeCase("c3_sample", case.q[idx], case.k, case.v, [case.block_tables[i] for i in idx],
+                               [case.seq_lens[i] for i in idx], 16, case.scale, case.kv_dtype)
+    ref = oracle_decode(sub, kc, vc, ks, vs)
+    assert_close(out[idx].float().cpu().numpy(), ref, torch.bfloat16, "c3 sample")
+
+
+def test_hal_backend_paged_attention(gpu):
+    from python_runtime.hal import registry
+    from python_runtime.hal.hip_backend import HipBackend, register_hip_backend
+
+    register_hip_backend()
+    be = registry.create("hip")
+    assert isinstance(be, HipBackend)
+    case = workloads.make_case("c3_llama3_8b", device=gpu, seed=9, batch=3)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    out = be.execute("paged_attention", [case.q, kc, vc, case.tables_tensor(gpu), case.seq_lens_tensor(gpu)],
+                     k_scale=ks, v_scale=vs, scale=case.scale)
+    torch.cuda.synchronize()
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, "hal")

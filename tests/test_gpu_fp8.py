@@ -1,0 +1,117 @@
+"""GPU FP8 quantization: codes and scales bit-identical to the CPU oracle.
+
+Covers the device e4m3fn encoder on all 2^32 float32 bit patterns, per-head
+and per-block scales (outliers, all-zero heads, the 1e-12 clamp, bf16/fp16/
+fp32 inputs), exact dequantization, the paged KV write (int32/int64 slots,
+skipped slots, both layouts) and the reference's TestFP8KVCache cases
+(tests/test_quantize.py:289-337 of the reference) on the device.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from cf_hip import layout as L
+from cf_hip import ops
+from kernels.quantize import FP8KVCacheQuantizer
+from oracle import fp8 as ofp8
+from tests.gpu_util import codes
+
+pytestmark = pytest.mark.gpu
+
+
+def test_device_encoder_exhaustive(gpu):
+    one = torch.ones(1, dtype=torch.float32, device=gpu)  # x / 1.0 == x exactly
+    chunk = 1 << 28
+    bad = 0
+    for start in range(0, 1 << 32, chunk):
+        bits = torch.arange(start, start + chunk, dtype=torch.int64, device=gpu).to(torch.int32)
+        got = ops.fp8_quantize(bits.view(torch.float32).view(1, 1, -1), one).view(torch.uint8).view(-1).cpu().numpy()
+        want = ofp8.encode_bits(start, chunk)
+        bad += int(np.count_nonzero(got != want))
+        del bits
+    print(f"[fp8] exhaustive mismatches: {bad}", flush=True)
+    assert bad == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_per_head_quantize_bit_exact(gpu, dtype):
+    g = torch.Generator(device=gpu).manual_seed(1)
+    x = torch.randn(3000, 8, 128, generator=g, device=gpu)
+    x = torch.where(torch.rand(x.shape, generator=g, device=gpu) < 0.01, x * 8, x)
+    x = x * torch.logspace(-14, 4, 8, device=gpu).view(1, 8, 1)
+    x[:, 5] = 0.0
+    x[7, 6, 3] = -0.0
+    x = x.to(dtype)
+    scales = ops.fp8_amax_scale(x)
+    q = ops.fp8_quantize(x, scales)
+    torch.cuda.synchronize()
+    want_codes, want_scales = ofp8.quantize_per_head(x.float().cpu().numpy())
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), want_scales.view(np.uint32))
+    assert np.array_equal(codes(q), want_codes)
+    assert scales[5].item() == 1.0
+
+
+def test_quantize_block_and_dequantize_bit_exact(gpu):
+    quant = FP8KVCacheQuantizer(block_size=16)
+    g = torch.Generator(device=gpu).manual_seed(2)
+    for i in range(20):
+        x = torch.randn(16, 8, 128, generator=g, device=gpu) * 10.0 ** (i - 12)
+        q, s = quant.quantize_block(x)
+        wc, ws = ofp8.quantize_block(x.cpu().numpy())
+        assert s.dim() == 0 and s.dtype == torch.float32
+        assert np.float32(s.item()).view(np.uint32) == ws.view(np.uint32)
+        assert np.array_equal(codes(q), wc)
+        deq = quant.dequantize_block(q, s)
+        assert np.array_equal(deq.cpu().numpy().view(np.uint32), ofp8.dequantize(wc, ws).view(np.uint32))
+
+
+def test_reference_fp8_cases_on_device(gpu):
+    quant = FP8KVCacheQuantizer(block_size=16)
+    torch.manual_seed(42)
+    k = torch.randn(16, 8, 128).to(gpu)
+    v = torch.randn(16, 8, 128).to(gpu)
+    kq, ks, vq, vs = quant.quantize_kv(k, v)
+    kf, vf = quant.dequantize_kv(kq, ks, vq, vs)
+    cos = torch.nn.functional.cosine_similarity
+    assert cos(k.flatten()[None], kf.flatten()[None]).item() >= 0.99
+    assert cos(v.flatten()[None], vf.flatten()[None]).item() >= 0.99
+    z = torch.zeros(16, 4, 64, device=gpu)
+    zq, zs = quant.quantize_block(z)
+    assert torch.allclose(quant.dequantize_block(zq, zs), z, atol=1e-6) and zs.item() == 1.0
+    small = torch.randn(4, 2, 32, device=gpu) * 0.02
+    sq, ss = FP8KVCacheQuantizer(block_size=4).quantize_block(small)
+    assert cos(small.flatten()[None], quant.dequantize_block(sq, ss).flatten()[None]).item() >= 0.95
+    assert quant.check_hardware_support("AMD MI300") and quant.check_hardware_support("AMD Instinct MI355X")
+    assert not quant.check_hardware_support("NVIDIA A100") and not quant.check_hardware_support("CPU")
+
+
+@pytest.mark.parametrize("layout", ["native", "token_major"])
+@pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
+def test_kv_write_bit_exact(gpu, layout, slot_dtype):
+    nb, bs, h, d, t = 40, 16, 8, 128, 300
+    g = torch.Generator(device=gpu).manual_seed(3)
+    kc, vc = L.alloc_kv_cache(nb, bs, h, d, torch.float8_e4m3fn, gpu, layout)
+    kc.view(torch.uint8).fill_(0xAA)
+    vc.view(torch.uint8).fill_(0xAA)
+    k_new = torch.randn(t, h, d, generator=g, device=gpu).to(torch.bfloat16)
+    v_new = torch.randn(t, h, d, generator=g, device=gpu).to(torch.bfloat16)
+    ks = ops.fp8_amax_scale(k_new)
+    vs = ops.fp8_amax_scale(v_new)
+    slots = torch.randperm(nb * bs, generator=torch.Generator().manual_seed(4))[:t]
+    slots[::37] = -1
+    FP8KVCacheQuantizer.write_kv_fp8(k_new, v_new, slots.to(gpu, slot_dtype), kc, vc, ks, vs)
+    torch.cuda.synchronize()
+    kcodes, vcodes = codes(kc), codes(vc)
+    wk = ofp8.quantize_per_head(k_new.float().cpu().numpy())[0]
+    wv = ofp8.quantize_per_head(v_new.float().cpu().numpy())[0]
+    written = np.zeros((nb, bs), dtype=bool)
+    for i, s in enumerate(slots.tolist()):
+        if s < 0:
+            continue
+        written[s // bs, s % bs] = True
+        assert np.array_equal(kcodes[s // bs, s % bs], wk[i])
+        assert np.array_equal(vcodes[s // bs, s % bs], wv[i])
+    assert np.all(kcodes[~written] == 0xAA) and np.all(vcodes[~written] == 0xAA)

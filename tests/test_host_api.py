@@ -1,0 +1,135 @@
+"""Host-side behaviour that needs no GPU: the reference-shaped Python API
+refuses CPU tensors (there is no CPU fallback), the FP8 quantizer's
+configuration rules, the HAL registry and HipBackend dispatch, KV layouts
+and the seeded workloads."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from cf_hip import layout as L
+from cf_hip import workloads
+from kernels.paged_attention import paged_attention, paged_attention_tensors
+from kernels.quantize import FP8KVCacheQuantizer
+from python_runtime.hal import registry
+from python_runtime.hal.hip_backend import HipBackend
+from python_runtime.hal.interface import OpExecutor
+
+
+def test_cpu_tensors_are_refused():
+    q = torch.randn(1, 4, 32)
+    k = torch.randn(4, 16, 4, 32)
+    with pytest.raises(ValueError, match="ROCm"):
+        paged_attention(q, k, k, {"r": [0]}, {"r": 5})
+    with pytest.raises(ValueError, match="ROCm"):
+        paged_attention_tensors(q, k, k, torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32))
+    with pytest.raises(ValueError, match="ROCm"):
+        FP8KVCacheQuantizer().quantize_block(k)
+
+
+def test_quantizer_configuration():
+    with pytest.raises(ValueError, match="block_size"):
+        FP8KVCacheQuantizer(block_size=0)
+    q = FP8KVCacheQuantizer(block_size=8)
+    assert q.block_size == 8 and q.fp8_max == 448.0 and q._has_fp8_dtype()
+    assert q.check_hardware_support("NVIDIA H100") and q.check_hardware_support("AMD MI300")
+    assert q.check_hardware_support("AMD Instinct MI355X")
+    assert not q.check_hardware_support("NVIDIA A100") and not q.check_hardware_support("CPU")
+    for hw in ("H100", "H200", "RTX_4090", "RTX_6000_ADA", "MI300"):
+        assert hw in q.SUPPORTED_HARDWARE
+
+
+def test_compiler_quantize_reexport():
+    from compiler.quantize import FP8KVCacheQuantizer as A
+    from compiler.quantize.fp8_kv_cache import FP8KVCacheQuantizer as B
+
+    assert A is FP8KVCacheQuantizer and B is FP8KVCacheQuantizer
+
+
+class _Recorder(OpExecutor):
+    def __init__(self):
+        self.calls = []
+
+    def execute(self, op_name, inputs, **kwargs):
+        self.calls.append((op_name, len(inputs), kwargs))
+        return torch.zeros(1)
+
+
+def test_registry_semantics():
+    name = "test_backend_xyz"
+    registry.register(name, lambda **kw: _Recorder())
+    with pytest.raises(ValueError, match="already registered"):
+        registry.register(name, lambda **kw: _Recorder())
+    assert isinstance(registry.create(name), _Recorder)
+    assert name in registry.list_backends()
+    with pytest.raises(KeyError):
+        registry.create("no_such_backend")
+    with pytest.raises(KeyError):
+        registry.get("no_such_backend")
+
+
+def test_hip_backend_dispatch_and_errors():
+    fb = _Recorder()
+    be = HipBackend(fallback=fb)
+    be.execute("silu", [torch.zeros(2)], alpha=1)
+    assert fb.calls == [("silu", 1, {"alpha": 1})]
+    with pytest.raises(ValueError, match="Unknown op"):
+        HipBackend().execute("silu", [torch.zeros(2)])
+    with pytest.raises(ValueError, match="at least 4"):
+        be.execute("paged_attention", [torch.zeros(1)])
+    with pytest.raises(ValueError, match="at most 5"):
+        be.execute("paged_attention", [torch.zeros(1)] * 6)
+    with pytest.raises(NotImplementedError):
+        be.async_copy(None, None, 0)
+    with pytest.raises(NotImplementedError):
+        be.memory_retrieve(None, None)
+    with pytest.raises(NotImplementedError):
+        be.send_kv_cache(None, "x")
+    assert "paged_attention" in HipBackend.supported_ops()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
+def test_layouts(dtype):
+    k, v = L.alloc_kv_cache(5, 16, 4, 32, dtype, "cpu", "native")
+    assert k.shape == v.shape == (5, 16, 4, 32)
+    assert k.stride() == (4 * 16 * 32, 32, 16 * 32, 1)
+    assert v.stride() == (4 * 32 * 16, 1, 32 * 16, 16)
+    assert L.layout_of(k, False) == "native" and L.layout_of(v, True) == "native"
+    src = torch.randn(5, 16, 4, 32)
+    for lay in L.LAYOUTS:
+        for is_v in (False, True):
+            t = L.to_layout(src, lay, is_v)
+            assert torch.equal(t, src) and L.layout_of(t, is_v) == lay
+    with pytest.raises(ValueError):
+        L.alloc_kv_cache(1, 16, 1, 8, torch.float32, "cpu", "bogus")
+
+
+def test_workloads_are_seeded_and_shaped():
+    a = workloads.make_case("c3_llama3_8b", seed=1, batch=4)
+    b = workloads.make_case("c3_llama3_8b", seed=1, batch=4)
+    assert a.block_tables == b.block_tables and a.seq_lens == b.seq_lens and torch.equal(a.k, b.k)
+    pre = a.meta["shared_prefix_blocks"]
+    assert pre == 64 and a.block_tables[0][:pre] == a.block_tables[1][:pre]
+    assert not set(a.block_tables[2]) & set(a.block_tables[0])
+    assert all(1024 <= n <= 8192 for n in a.seq_lens)
+    assert a.q.shape == (4, 32, 128) and a.k.shape[1:] == (16, 8, 128) and a.kv_dtype == torch.float8_e4m3fn
+    c4 = workloads.make_case("c4_llama3_70b", seed=1, batch=16)
+    assert all(512 <= n <= 32768 for n in c4.seq_lens) and c4.q.shape[1] == 64
+    c1 = workloads.make_case("c1_opt125m", seed=1)
+    flat = [b for t in c1.block_tables for b in t]
+    assert len(flat) == len(set(flat)) and all(0 <= x < 256 for x in flat)
+    with pytest.raises(ValueError):
+        workloads.make_case("nope")
+
+
+def test_algorithmic_bytes():
+    q = torch.zeros(2, 4, 8, dtype=torch.bfloat16)
+    k = torch.zeros(4, 16, 2, 8, dtype=torch.bfloat16)
+    case = workloads.DecodeCase("t", q, k, k, [[0, 1], [0, 2]], [20, 30], 16, 0.1, torch.float8_e4m3fn)
+    ab = workloads.algorithmic_bytes(case)
+    per_tok = 2 * 2 * 8 * 1
+    # block 0: 16 rows (shared), block 1: 4 rows, block 2: 14 rows
+    assert ab["unique_kv"] == (16 + 4 + 14) * per_tok
+    assert ab["logical"] - ab["unique"] == (50 - 34) * per_tok
+    assert ab["tokens"] == 50
