@@ -217,6 +217,7 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache, const CfTens
   CF_CHECK(vk.size[3] == D, "k_cache head_dim %lld differs from q head_dim %lld", (long long)vk.size[3],
            (long long)D);
   CF_CHECK(bs == block_size, "k_cache block dim %lld differs from block_size %d", (long long)bs, block_size);
+  CF_CHECK(Hq > 0, "q has no heads");
   CF_CHECK(Hkv > 0 && Hq % Hkv == 0, "num_heads %lld is not a multiple of num_kv_heads %lld", (long long)Hq,
            (long long)Hkv);
   CF_CHECK(D > 0 && D <= 512, "head_dim %lld out of range (1..512)", (long long)D);
@@ -259,6 +260,7 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache, const CfTens
   p.D = (int)D;
   p.bs = block_size;
   p.Mb = (int)vt.size[1];
+  p.NB = (int)NB;
   p.PT = partition_tokens;
   p.max_parts = (int)decode_max_parts(vt.size[1], block_size, partition_tokens);
 
@@ -385,6 +387,7 @@ int32_t cf_kv_write_fp8(const CfTensor* k_new, const CfTensor* v_new, const CfTe
   p.H = (int)H;
   p.D = (int)D;
   p.bs = (int)vkc.size[1];
+  p.NB = vkc.size[0];
   return launch_kv_write_fp8(p, vk.dtype, vsl.dtype, as_stream(stream));
 }
 

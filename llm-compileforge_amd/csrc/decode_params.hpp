@@ -27,6 +27,7 @@ struct DecodeParams {
   float* ws_ml;        // [B, Hq, max_parts, 2] running max and sum
   float scale;
   int B, Hq, Hkv, G, D, bs, Mb, PT, max_parts;
+  int NB;  // cache blocks; a block id outside [0, NB) contributes no tokens
 };
 
 // Launchers (return a CF_* status; kernels are enqueued on `stream`).

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteParams p) {
   int64_t slot;
   if (ST == kI64) slot = ((const int64_t*)p.slots)[i * p.slot_stride];
   else slot = ((const int32_t*)p.slots)[i * p.slot_stride];
-  if (slot < 0) return;
+  if (slot < 0 || slot >= p.NB * p.bs) return;
   const int64_t blk = slot / p.bs, off = slot % p.bs;
   using XE = Elem<XT>;
   const int n = p.H * p.D;

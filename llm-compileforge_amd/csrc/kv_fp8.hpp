@@ -25,6 +25,7 @@ struct KvWriteParams {
   const float* v_scale;
   int64_t ks_s, vs_s;
   int64_t T;
+  int64_t NB;  // cache blocks; slots outside [0, NB * bs) are skipped
   int H, D, bs;
 };
 

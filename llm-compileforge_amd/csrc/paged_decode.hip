@@ -74,6 +74,10 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
   for (int i = tid; i < count; i += kGenericThreads) {
     const int tok = start + i;
     const int64_t blk = sblk[i / bs];
+    if ((uint32_t)blk >= (uint32_t)p.NB) {
+      for (int g = 0; g < G; ++g) sc[g * PT + i] = -INFINITY;
+      continue;
+    }
     const typename KE::T* krow =
         kbase + blk * p.k_s[0] + (int64_t)(tok % bs) * p.k_s[1] + (int64_t)h * p.k_s[2];
     for (int g = 0; g < G; ++g) {
@@ -94,7 +98,7 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
     m = wave_max(m);
     float l = 0.0f;
     for (int i = lane; i < count; i += 64) {
-      const float e = expf(sc[g * PT + i] - m);
+      const float e = m == -INFINITY ? 0.0f : expf(sc[g * PT + i] - m);
       sc[g * PT + i] = e;
       l += e;
     }
@@ -114,6 +118,7 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
     for (int t = 0; t < count; ++t) {
       const int tok = start + t;
       const int64_t blk = sblk[t / bs];
+      if ((uint32_t)blk >= (uint32_t)p.NB) continue;
       const typename KE::T* vrow =
           vbase + blk * p.v_s[0] + (int64_t)(tok % bs) * p.v_s[1] + (int64_t)h * p.v_s[2];
       acc = fmaf(sc[g * PT + t], KE::load(vrow + (int64_t)d * p.v_s[3]), acc);
@@ -121,8 +126,9 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
     acc *= vs;
     const int hq = h * G + g;
     if (DIRECT) {
+      const float l = sml[2 * g + 1];
       OutE::store((typename OutE::T*)p.out + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d,
-                  acc / sml[2 * g + 1]);
+                  l > 0.0f ? acc / l : 0.0f);
     } else {
       const int64_t row = ((int64_t)b * p.Hq + hq) * p.max_parts + part;
       p.ws_o[row * D + d] = acc;
@@ -150,13 +156,19 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
   }
   float M = -INFINITY;
   for (int i = 0; i < nparts; ++i) M = fmaxf(M, p.ws_ml[(row0 + i) * 2]);
+  // A partition whose blocks were all invalid has m = -inf and l = 0.
   float L = 0.0f;
-  for (int i = 0; i < nparts; ++i) L += p.ws_ml[(row0 + i) * 2 + 1] * expf(p.ws_ml[(row0 + i) * 2] - M);
-  const float inv = 1.0f / L;
+  for (int i = 0; i < nparts; ++i) {
+    const float m = p.ws_ml[(row0 + i) * 2];
+    if (m != -INFINITY) L += p.ws_ml[(row0 + i) * 2 + 1] * expf(m - M);
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
     float acc = 0.0f;
-    for (int i = 0; i < nparts; ++i)
-      acc = fmaf(expf(p.ws_ml[(row0 + i) * 2] - M), p.ws_o[(row0 + i) * p.D + d], acc);
+    for (int i = 0; i < nparts; ++i) {
+      const float m = p.ws_ml[(row0 + i) * 2];
+      if (m != -INFINITY) acc = fmaf(expf(m - M), p.ws_o[(row0 + i) * p.D + d], acc);
+    }
     OutE::store(o + d, acc * inv);
   }
 }
