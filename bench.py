@@ -134,9 +134,14 @@ def main() -> None:
             plans[i % len(plans)].run()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-    dec_ms, dec_n = timer.query("cf_decode_")
-    red_ms, red_n = timer.query("cf_decode_reduce")
-    main_ms, main_n = dec_ms - red_ms, dec_n - red_n
+    main_ms, main_n = timer.query("cf_decode_mfma")
+    kernel_name = "cf_decode_mfma"
+    if main_n == 0:
+        main_ms, main_n = timer.query("cf_decode_generic")
+        kernel_name = "cf_decode_generic"
+    red_ms, red_n = timer.query("cf_decode_merge")
+    r2_ms, r2_n = timer.query("cf_decode_reduce")
+    red_ms, red_n = red_ms + r2_ms, red_n + r2_n
     timer.reset()
     ms_step = (t1 - t0) * 1e3 / args.steps
     log(f"{ms_step * 1e3:.1f} us/step; decode kernel {main_ms / max(main_n, 1) * 1e3:.1f} us, "
@@ -174,7 +179,8 @@ def main() -> None:
         },
         "hbm_gbs_step": ab["unique"] / (ms_step / 1e3) / 1e9,
         "hbm_frac_step": ab["unique"] / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS,
-        "kernel_us": {"decode": avg_main_s * 1e6, "reduce": red_ms / max(red_n, 1) * 1e3},
+        "kernel_us": {"decode": avg_main_s * 1e6, "merge": red_ms / max(red_n, 1) * 1e3,
+                      "decode_kernel": kernel_name},
         "algorithmic_bytes": {"unique": ab["unique"], "logical": ab["logical"]},
         "roofline": {
             "bound": "hbm",

@@ -67,11 +67,13 @@ int32_t cf_abi_version(void);
  * truncated to len) and returns the full message length. */
 int32_t cf_last_error(char* buf, uint64_t len);
 
-/* Workspace needed by cf_paged_decode for a batch whose block tables hold at
- * most max_blocks_per_seq entries.  Replaces no reference function: the
- * reference decode (kernels/paged_attention.py:21-73) gathers into
- * temporaries; this path splits long contexts into partitions instead. */
+/* Workspace needed by cf_paged_decode (on the current device) for a batch
+ * whose block tables hold at most max_blocks_per_seq entries.  Replaces no
+ * reference function: the reference decode (kernels/paged_attention.py
+ * :21-73) gathers into temporaries; this path splits long contexts across
+ * waves and merges (m, l, o) partials instead. */
 int32_t cf_paged_decode_workspace_bytes(int64_t batch, int64_t num_q_heads,
+                                        int64_t num_kv_heads,
                                         int64_t head_dim,
                                         int64_t max_blocks_per_seq,
                                         int32_t block_size,
@@ -95,10 +97,21 @@ int32_t cf_paged_decode_workspace_bytes(int64_t batch, int64_t num_q_heads,
  *
  * Sequence b attends to its first min(seq_lens[b], Mb*bs) tokens, read
  * through block_tables[b]; query head h uses KV head h / (Hq/Hkv).
- * Sequences of length 0 produce zeros.  Block ids must be < NB (not
- * checked on the device; the Python layer checks host-side tables).
- * partition_tokens (multiple of bs, >= bs) splits a sequence across
- * workgroups; the partials are merged by a log-sum-exp reduce. */
+ * Sequences of length 0 produce zeros.  A block id outside [0, NB)
+ * contributes no tokens (the dict-based Python API rejects such tables
+ * before the call, as the reference's indexing would).
+ *
+ * With bf16 q, bf16/e4m3fn caches, bs = 16, head_dim 64 or 128, G <= 16,
+ * K rows with unit channel stride and V stored channel-major inside a
+ * block (token stride 1: the layout cf_hip.layout calls "native"), one
+ * MFMA kernel balances 32-token tiles evenly over all waves of the GPU and
+ * a merge kernel combines the sequences split between waves;
+ * partition_tokens is unused there.  Other inputs run a generic kernel that
+ * splits sequences into partition_tokens partitions (multiple of bs)
+ * merged by a log-sum-exp reduce.
+ *
+ * workspace: cf_paged_decode_workspace_bytes() bytes, 256-byte aligned;
+ * calls that share a workspace must not overlap. */
 int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache,
                         const CfTensor* v_cache, const CfTensor* block_tables,
                         const CfTensor* seq_lens, const CfTensor* k_scale,
@@ -111,20 +124,22 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache,
  * at 1e-12, and 1.0 where amax == 0.  This is
  * FP8KVCacheQuantizer.quantize_block's scale rule (reference
  * compiler/quantize/fp8_kv_cache.py:81-86) applied per KV head.
- *   x       [T, H, Dx]  f32 | f16 | bf16
- *   scales  [H]         f32 (output) */
+ *   x       [T, H, Dx] or [S0, S1, H, Dx]  f32 | f16 | bf16
+ *   scales  [H]         f32 (output, contiguous) */
 int32_t cf_fp8_amax_scale(const CfTensor* x, CfTensor* scales, void* stream);
 
 /* out[t,h,d] = e4m3fn(f32(x[t,h,d]) / scales[h]) with IEEE division and
  * round-to-nearest-even, |v| >= 480 -> NaN code (torch's float8_e4m3fn
  * conversion).  Reference compiler/quantize/fp8_kv_cache.py:89.
- *   x [T,H,Dx] f32|f16|bf16; scales [H] or [1] f32; out [T,H,Dx] e4m3fn */
+ *   x [T,H,Dx] or [S0,S1,H,Dx] f32|f16|bf16; scales [H] or [1] f32;
+ *   out: e4m3fn, same shape (any strides) */
 int32_t cf_fp8_quantize(const CfTensor* x, const CfTensor* scales,
                         CfTensor* out, void* stream);
 
 /* out[t,h,d] = f32(q[t,h,d]) * scales[h].
  * Reference compiler/quantize/fp8_kv_cache.py:95-105.
- *   q [T,H,Dx] e4m3fn; scales [H] or [1] f32; out [T,H,Dx] f32 */
+ *   q [T,H,Dx] or [S0,S1,H,Dx] e4m3fn; scales [H] or [1] f32;
+ *   out: f32, same shape */
 int32_t cf_fp8_dequantize(const CfTensor* q, const CfTensor* scales,
                           CfTensor* out, void* stream);
 
@@ -132,7 +147,7 @@ int32_t cf_fp8_dequantize(const CfTensor* q, const CfTensor* scales,
  * per-head scales: token i goes to block slot_mapping[i] / bs, offset
  * slot_mapping[i] % bs (reference token placement:
  * python_runtime/engine/cache_manager.py:139-171, _kv_cache.py:68-104);
- * slots < 0 are skipped.
+ * slots < 0 or >= NB * bs are skipped.
  *   k_new, v_new  [T, Hkv, D]       f32 | f16 | bf16
  *   slot_mapping  [T]               i32 | i64
  *   k_cache,      [NB, bs, Hkv, D]  e4m3fn, any strides

@@ -132,8 +132,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "cf_last_error": (ctypes.c_int32, [ctypes.c_char_p, ctypes.c_uint64]),
     "cf_paged_decode_workspace_bytes": (
         ctypes.c_int32,
-        [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
-         ctypes.POINTER(ctypes.c_uint64)],
+        [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+         ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)],
     ),
     "cf_paged_decode": (
         ctypes.c_int32,

@@ -33,15 +33,35 @@ def _same_device(*ts: torch.Tensor) -> torch.device:
 
 
 def decode_workspace_bytes(
-    batch: int, num_q_heads: int, head_dim: int, max_blocks_per_seq: int, block_size: int,
+    batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_blocks_per_seq: int, block_size: int,
     partition_tokens: int = DEFAULT_PARTITION_TOKENS,
 ) -> int:
     out = ctypes.c_uint64(0)
     rc = lib().cf_paged_decode_workspace_bytes(
-        batch, num_q_heads, head_dim, max_blocks_per_seq, block_size, partition_tokens, ctypes.byref(out)
+        batch, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size, partition_tokens,
+        ctypes.byref(out),
     )
     check(rc, "cf_paged_decode_workspace_bytes")
     return int(out.value)
+
+
+def new_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """A decode workspace of at least `nbytes` bytes (256-byte aligned)."""
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
+# One workspace per (device, stream) for callers that pass none: calls on
+# one stream run in order, so they may share it.
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _cached_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle(device))
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = new_workspace(nbytes, device)
+        _WORKSPACES[key] = ws
+    return ws
 
 
 def paged_decode(
@@ -60,6 +80,9 @@ def paged_decode(
 ) -> torch.Tensor:
     """Paged decode attention on the GPU; returns out [B, Hq, D] (dtype of q).
 
+    workspace: optional buffer of decode_workspace_bytes() bytes; by default
+    a cached one per (device, stream) is used.
+
     block_tables: int32 [B, Mb]; seq_lens: int32 [B]; caches [NB, bs, Hkv, D]
     with any strides (f32/f16/bf16/e4m3fn); e4m3fn caches need per-KV-head
     fp32 k_scale/v_scale of shape [Hkv] or [1].
@@ -71,12 +94,14 @@ def paged_decode(
     if out is None:
         out = torch.empty(q.shape, dtype=q.dtype, device=dev)
     need = decode_workspace_bytes(
-        q.shape[0], q.shape[1], q.shape[2], block_tables.shape[1], block_size, partition_tokens
+        q.shape[0], q.shape[1], k_cache.shape[2], q.shape[2], block_tables.shape[1], block_size, partition_tokens
     )
     ws_ptr = None
     if need > 0:
-        if workspace is None or workspace.numel() * workspace.element_size() < need:
-            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        if workspace is None:
+            workspace = _cached_workspace(need, dev)
+        elif workspace.numel() * workspace.element_size() < need:
+            raise ValueError(f"workspace of {need} bytes needed, {workspace.numel() * workspace.element_size()} given")
         ws_ptr = workspace.data_ptr()
     ks = descriptor(k_scale) if k_scale is not None else None
     vs = descriptor(v_scale) if v_scale is not None else None
@@ -120,9 +145,10 @@ class DecodePlan:
         self.device = _same_device(q, k_cache, v_cache, block_tables, seq_lens)
         self.out = out if out is not None else torch.empty(q.shape, dtype=q.dtype, device=self.device)
         self.ws_bytes = decode_workspace_bytes(
-            q.shape[0], q.shape[1], q.shape[2], block_tables.shape[1], block_size, partition_tokens
+            q.shape[0], q.shape[1], k_cache.shape[2], q.shape[2], block_tables.shape[1], block_size,
+            partition_tokens,
         )
-        self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=self.device)
+        self.workspace = new_workspace(self.ws_bytes, self.device)
         self._keep = (q, k_cache, v_cache, block_tables, seq_lens, k_scale, v_scale)
         self._d = [descriptor(t) for t in (q, k_cache, v_cache, block_tables, seq_lens)]
         self._ks = descriptor(k_scale) if k_scale is not None else None
@@ -245,6 +271,7 @@ __all__ = [
     "DecodePlan",
     "KernelTimer",
     "decode_workspace_bytes",
+    "new_workspace",
     "fp8_amax_scale",
     "fp8_dequantize",
     "fp8_quantize",

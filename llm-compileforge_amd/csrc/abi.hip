@@ -166,24 +166,30 @@ static int64_t decode_max_parts(int64_t max_blocks, int32_t bs, int32_t pt) {
   return std::max<int64_t>(1, ceil_div(max_blocks * (int64_t)bs, pt));
 }
 
-int32_t cf_paged_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim,
-                                        int64_t max_blocks_per_seq, int32_t block_size,
+// Generic-path layout: [o partials, 256-byte padded] [(m, l)].
+static uint64_t generic_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t parts) {
+  if (parts <= 1) return 0;
+  const uint64_t rows = (uint64_t)batch * num_q_heads * parts;
+  const uint64_t o_bytes = rows * head_dim * 4;
+  const uint64_t ml_bytes = rows * 2 * 4;
+  return ((o_bytes + 255) & ~(uint64_t)255) + ml_bytes;
+}
+
+int32_t cf_paged_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                        int64_t head_dim, int64_t max_blocks_per_seq, int32_t block_size,
                                         int32_t partition_tokens, uint64_t* bytes_out) {
   CF_CHECK(bytes_out != nullptr, "bytes_out is NULL");
-  CF_CHECK(batch >= 0 && num_q_heads > 0 && head_dim > 0 && max_blocks_per_seq >= 0,
+  CF_CHECK(batch >= 0 && num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && max_blocks_per_seq >= 0,
            "invalid sizes");
+  CF_CHECK(num_q_heads % num_kv_heads == 0, "num_heads %lld is not a multiple of num_kv_heads %lld",
+           (long long)num_q_heads, (long long)num_kv_heads);
   CF_CHECK(block_size > 0 && partition_tokens > 0 && partition_tokens % block_size == 0,
            "partition_tokens (%d) must be a positive multiple of block_size (%d)", partition_tokens,
            block_size);
   const int64_t parts = decode_max_parts(max_blocks_per_seq, block_size, partition_tokens);
-  if (parts <= 1) {
-    *bytes_out = 0;
-    return CF_OK;
-  }
-  const uint64_t rows = (uint64_t)batch * num_q_heads * parts;
-  const uint64_t o_bytes = rows * head_dim * 4;
-  const uint64_t ml_bytes = rows * 2 * 4;
-  *bytes_out = ((o_bytes + 255) & ~(uint64_t)255) + ml_bytes;
+  const uint64_t generic = generic_workspace_bytes(batch, num_q_heads, head_dim, parts);
+  const uint64_t mfma = block_size == 16 ? decode_mfma_workspace_bytes(num_q_heads, num_kv_heads, head_dim) : 0;
+  *bytes_out = generic > mfma ? generic : mfma;
   return CF_OK;
 }
 
@@ -273,8 +279,9 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache, const CfTens
   }
   if (B == 0) return CF_OK;
 
-  uint64_t need = 0;
-  if ((rc = cf_paged_decode_workspace_bytes(B, Hq, D, vt.size[1], block_size, partition_tokens, &need))) return rc;
+  const bool mfma = decode_mfma_supported(p, vq.dtype, vk.dtype);
+  const uint64_t need = mfma ? decode_mfma_workspace_bytes(Hq, Hkv, D)
+                             : generic_workspace_bytes(B, Hq, D, p.max_parts);
   if (need > 0) {
     if (workspace == nullptr || workspace_bytes < need) {
       set_error("workspace of %llu bytes needed, %llu given", (unsigned long long)need,
@@ -282,17 +289,19 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache, const CfTens
       return CF_ERR_WORKSPACE;
     }
     CF_CHECK(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
-    const uint64_t rows = (uint64_t)B * Hq * p.max_parts;
-    p.ws_o = (float*)workspace;
-    p.ws_ml = (float*)((char*)workspace + (((rows * D * 4) + 255) & ~(uint64_t)255));
+    if (mfma) {
+      decode_mfma_bind_workspace(p, workspace);
+    } else {
+      const uint64_t rows = (uint64_t)B * Hq * p.max_parts;
+      char* base = (char*)workspace;
+      p.ws_o = (float*)base;
+      p.ws_ml = (float*)(base + (((rows * D * 4) + 255) & ~(uint64_t)255));
+    }
   }
 
   hipStream_t st = as_stream(stream);
-  if (decode_mfma_supported(p, vq.dtype, vk.dtype)) {
-    rc = launch_decode_mfma(p, vq.dtype, vk.dtype, st);
-  } else {
-    rc = launch_decode_generic(p, vq.dtype, vk.dtype, st);
-  }
+  if (mfma) return launch_decode_mfma(p, vq.dtype, vk.dtype, st);
+  rc = launch_decode_generic(p, vq.dtype, vk.dtype, st);
   if (rc) return rc;
   if (p.max_parts > 1) rc = launch_decode_reduce(p, vq.dtype, st);
   return rc;

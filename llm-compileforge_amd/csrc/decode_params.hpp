@@ -34,6 +34,10 @@ struct DecodeParams {
 int32_t launch_decode_generic(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream);
 int32_t launch_decode_mfma(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream);
 bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt);
+// Workspace of the MFMA path: two (m, l, o) partial slots per launched wave.
+uint64_t decode_mfma_workspace_bytes(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim);
+void decode_mfma_bind_workspace(DecodeParams& p, void* workspace);
+
 int32_t launch_decode_reduce(const DecodeParams& p, int q_dt, hipStream_t stream);
 
 }  // namespace cf

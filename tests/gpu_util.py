@@ -20,14 +20,31 @@ def metrics(got: np.ndarray, ref: np.ndarray) -> tuple[float, float]:
     return err, cos
 
 
+def bf16_ulp(x: np.ndarray) -> np.ndarray:
+    """Spacing of the bfloat16 grid at |x| (8 significant bits)."""
+    a = np.maximum(np.abs(np.asarray(x, dtype=np.float64)), 2.0**-126)
+    return 2.0 ** (np.floor(np.log2(a)) - 7)
+
+
 def assert_close(got, ref, dtype: torch.dtype, what: str = "") -> None:
-    """fp32: max-abs <= 1e-5; bf16/fp16/fp8: max-abs <= 2e-2 and cosine >= 0.9999."""
+    """Parity against the float64 oracle.
+
+    fp32 outputs: max-abs <= 1e-5.  bf16 outputs (bf16 or e4m3 caches):
+    cosine >= 0.9999 and every element within max(2e-2, one bf16 ulp of the
+    exact value) -- an output stored in bfloat16 is off by up to half an ulp
+    from the exact value whatever computed it (0.03 at |o| = 14), so the
+    2e-2 bound applies where the bf16 grid is finer than it.
+    """
     err, cos = metrics(got, ref)
     print(f"[parity] {what} max_abs={err:.3e} cosine={cos:.7f}", flush=True)
     if dtype == torch.float32:
         assert err <= 1e-5, (what, err)
     else:
-        assert err <= 2e-2 and cos >= 0.9999, (what, err, cos)
+        g = np.asarray(got, dtype=np.float64)
+        r = np.asarray(ref, dtype=np.float64)
+        bound = np.maximum(2e-2, bf16_ulp(r))
+        excess = float((np.abs(g - r) - bound).max()) if g.size else 0.0
+        assert cos >= 0.9999 and excess <= 0.0, (what, err, cos, excess)
 
 
 def codes(t: torch.Tensor) -> np.ndarray:

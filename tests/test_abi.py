@@ -172,14 +172,19 @@ def test_fp8_cache_requires_scales_and_workspace_is_checked():
 def test_workspace_size_formula():
     n = ctypes.c_uint64()
     lib = _abi.lib()
-    assert lib.cf_paged_decode_workspace_bytes(64, 32, 128, 512, 16, 512, ctypes.byref(n)) == 0
-    parts = 512 * 16 // 512
+    # block size 8: the generic path only -> partition partials
+    assert lib.cf_paged_decode_workspace_bytes(64, 32, 8, 128, 32, 8, 512, ctypes.byref(n)) == 0
+    assert n.value == 0  # a single partition needs no workspace
+    assert lib.cf_paged_decode_workspace_bytes(64, 32, 8, 128, 1024, 8, 512, ctypes.byref(n)) == 0
+    parts = 1024 * 8 // 512
     rows = 64 * 32 * parts
     o = rows * 128 * 4
     assert n.value == ((o + 255) // 256) * 256 + rows * 8
-    assert lib.cf_paged_decode_workspace_bytes(64, 32, 128, 32, 16, 512, ctypes.byref(n)) == 0
-    assert n.value == 0  # a single partition needs no workspace
-    assert lib.cf_paged_decode_workspace_bytes(64, 32, 128, 32, 16, 24, ctypes.byref(n)) == _abi.CF_ERR_INVALID
+    # block size 16: at least the MFMA path's per-wave slots
+    assert lib.cf_paged_decode_workspace_bytes(64, 32, 8, 128, 32, 16, 512, ctypes.byref(n)) == 0
+    assert n.value > 0 and n.value % 8 == 0
+    assert lib.cf_paged_decode_workspace_bytes(64, 32, 8, 128, 32, 16, 24, ctypes.byref(n)) == _abi.CF_ERR_INVALID
+    assert lib.cf_paged_decode_workspace_bytes(64, 32, 5, 128, 32, 16, 512, ctypes.byref(n)) == _abi.CF_ERR_INVALID
 
 
 def test_fp8_entry_points_validate():

@@ -173,3 +173,59 @@ def test_hal_backend_paged_attention(gpu):
     torch.cuda.synchronize()
     ref = oracle_decode(case, kc, vc, ks, vs)
     assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, "hal")
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_long_single_sequence_split_over_many_waves(gpu, kv_dtype):
+    """One 30000-token sequence: every KV head's run is split over hundreds of
+    waves, so the merge combines more than 64 partials per head."""
+    print(f"[case] long single sequence kv={kv_dtype}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(12)
+    n, hq, hkv, d = 30000, 32, 8, 128
+    nb = (n + 15) // 16 + 3
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(3)).tolist()
+    q = torch.randn(1, hq, d, generator=g, device=gpu).to(torch.bfloat16)
+    ksrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
+    vsrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
+    case = workloads.DecodeCase("long", q, ksrc, vsrc, [perm[: (n + 15) // 16]], [n], 16, 1 / math.sqrt(d), kv_dtype)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    out = _run(case, kc, vc, ks, vs, gpu)
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, "long sequence")
+
+
+def test_repeated_calls_share_a_workspace(gpu):
+    """Repeated calls on one workspace give bit-identical outputs, also after
+    a call with another batch shape in between."""
+    case = workloads.make_case("c3_llama3_8b", device=gpu, seed=13, batch=16)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    tables, lens = case.tables_tensor(gpu), case.seq_lens_tensor(gpu)
+    need = ops.decode_workspace_bytes(16, 32, 8, 128, tables.shape[1], 16)
+    ws = ops.new_workspace(need, gpu)
+    outs = []
+    for i in range(4):
+        if i == 2:  # a differently shaped call in between
+            ops.paged_decode(case.q[:3], kc, vc, tables[:3], lens[:3], case.scale, 16, ks, vs, workspace=ws)
+        outs.append(ops.paged_decode(case.q, kc, vc, tables, lens, case.scale, 16, ks, vs, workspace=ws).clone())
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    assert_close(outs[0].float().cpu().numpy(), ref, torch.bfloat16, "repeated")
+
+
+def test_invalid_block_ids_contribute_nothing(gpu):
+    """Tensor API: a table entry outside [0, NB) drops that block's tokens."""
+    case = workloads.make_case("c3_llama3_8b", device=gpu, seed=14, batch=4)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    nb = kc.shape[0]
+    tables = case.tables_tensor(gpu)
+    bad = tables.clone()
+    bad[0, 3] = nb + 7  # a full middle block of sequence 0
+    bad[1, 5] = -2
+    out = _run(case, kc, vc, ks, vs, gpu, tables=bad)
+    t0 = case.block_tables[0][:3] + case.block_tables[0][4:]
+    t1 = case.block_tables[1][:5] + case.block_tables[1][6:]
+    lens = [case.seq_lens[0] - 16, case.seq_lens[1] - 16, case.seq_lens[2], case.seq_lens[3]]
+    ref = oracle_decode(case, kc, vc, ks, vs, tables=[t0, t1, case.block_tables[2], case.block_tables[3]], lens=lens)
+    assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, "invalid ids")
