@@ -6,7 +6,7 @@ Every .hip file in this directory is compiled with hipcc for gfx950 into
 _build/, then linked into ../cf_hip/libcf_hip.so.  Floating-point flags:
 no fast-math, fp32 division and sqrt correctly rounded, fp32 denormals kept
 (IEEE), so quantized FP8 codes match the CPU bit for bit.  Packed-fp32 VALU
-instructions are disabled.
+instructions are disabled.  MFMA results are kept in VGPRs (not AGPRs).
 """
 
 from __future__ import annotations
@@ -40,6 +40,10 @@ CFLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the decode loop rescales and stores its
+    # accumulators, and AGPR<->VGPR copies each tile cost more than they save.
+    "-Xarch_device",
+    "-mllvm=-amdgpu-mfma-vgpr-form",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]

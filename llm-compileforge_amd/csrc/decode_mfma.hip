@@ -82,29 +82,35 @@ struct TileRegs {
   VT v[NV];
 };
 
+// Loads one 32-token tile (blocks blkA, blkB of KV head h) in the native
+// layout: K tile [bs][D] (token rows), V tile [D][bs] (channel rows), each
+// (block, head) tile contiguous.  Inner offsets are compile-time constants
+// (immediate offsets of the loads); block/head strides are uniform.
+// Invalid blocks (id -1) read block 0 instead; their tokens are masked.
 template <int KT, int D>
 __device__ __forceinline__ void load_tile(TileRegs<KT, D>& r, const DecodeParams& p, const uint8_t* kbase,
                                           const uint8_t* vbase, int blkA, int blkB, int li, int lq, int h) {
   constexpr int KB = KvTraits<KT>::kBytes;
   using R = TileRegs<KT, D>;
-  const int tok1 = 8 * (li >> 2) + (li & 3);  // 0..27 within the tile; tok2 = tok1 + 4
-  // Invalid blocks (id -1) read block 0 instead; their tokens are masked.
-  const int kblk = max(tok1 < 16 ? blkA : blkB, 0);
-  const int koff = tok1 & 15;
-  const uint8_t* k1 = kbase + ((int64_t)kblk * p.k_s[0] + (int64_t)koff * p.k_s[1] + (int64_t)h * p.k_s[2] +
-                               (int64_t)lq * (D / 4)) * KB;
-  const uint8_t* k2 = k1 + (int64_t)4 * p.k_s[1] * KB;
+  const int64_t a = blkA < 0 ? 0 : blkA, bb = blkB < 0 ? 0 : blkB;
+  const uint8_t* kA = kbase + (a * p.k_s[0] + (int64_t)h * p.k_s[2]) * KB;
+  const uint8_t* kB = kbase + (bb * p.k_s[0] + (int64_t)h * p.k_s[2]) * KB;
+  const uint8_t* vA = vbase + (a * p.v_s[0] + (int64_t)h * p.v_s[2]) * KB;
+  const uint8_t* vB = vbase + (bb * p.v_s[0] + (int64_t)h * p.v_s[2]) * KB;
+  // K: lane (li, lq) reads token koff = 8*(li/4)%16 + li%4 (+4) of block A
+  // (li < 8) or B, channels [lq*D/4, (lq+1)*D/4).
+  const int koff = (8 * (li >> 2) + (li & 3)) & 15;
+  const uint8_t* k1 = (li < 8 ? kA : kB) + (koff * D + lq * (D / 4)) * KB;
 #pragma unroll
   for (int c = 0; c < R::KCHUNK; ++c) {
     r.k1[c] = *(const uint4*)(k1 + 16 * c);
-    r.k2[c] = *(const uint4*)(k2 + 16 * c);
+    r.k2[c] = *(const uint4*)(k1 + 4 * D * KB + 16 * c);
   }
-  const int vblk = max(lq < 2 ? blkA : blkB, 0);
-  const uint8_t* vp = vbase + ((int64_t)vblk * p.v_s[0] + (int64_t)(lq & 1) * 8 + (int64_t)h * p.v_s[2] +
-                               (int64_t)li * p.v_s[3]) * KB;
-  const int64_t vstep = (int64_t)16 * p.v_s[3] * KB;
+  // V: lane (li, lq) reads channel 16t + li, tokens 8*(lq%2)..+7 of block A
+  // (lq < 2) or B.
+  const uint8_t* vp = (lq < 2 ? vA : vB) + (li * 16 + (lq & 1) * 8) * KB;
 #pragma unroll
-  for (int t = 0; t < R::NV; ++t) r.v[t] = *(const typename R::VT*)(vp + t * vstep);
+  for (int t = 0; t < R::NV; ++t) r.v[t] = *(const typename R::VT*)(vp + t * 256 * KB);
 }
 
 // Keeps the first `nbytes` bytes of an 8-byte register pair, zeroing the rest.
@@ -135,8 +141,18 @@ __device__ __forceinline__ bf16x8_t k_operand(const uint4* raw, int c) {
   }
 }
 
-__device__ __forceinline__ bf16x8_t v_operand(uint2 raw) { return e4m3x8_to_bf16(raw.x, raw.y); }
-__device__ __forceinline__ bf16x8_t v_operand(uint4 raw) { return as_bf16x8(raw); }
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// 8 e4m3 codes -> 8 fp16 (exact: e4m3 values lie inside fp16's range and
+// precision).
+__device__ __forceinline__ f16x8_t e4m3x8_to_f16(uint32_t lo, uint32_t hi) {
+  uint4 r;
+  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false));
+  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true));
+  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false));
+  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true));
+  return __builtin_bit_cast(f16x8_t, r);
+}
 
 
 // ---------------------------------------------------------------------------
@@ -357,51 +373,76 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
       s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_operand<KT>(r0.k2, c), qop[c], s2, 0, 0, 0);
     }
     // lane (li, lq): s1[v] -> token 8lq + v, s2[v] -> token 8lq + 4 + v, head li
-    const int nvalid = c0.len - 32 * c0.j - 8 * lq;
-    const bool blk_ok = (lq < 2 ? c0.blkA : c0.blkB) >= 0;
     float sc[8];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      sc[v] = (blk_ok && v < nvalid) ? s1[v] * qk_scale : -INFINITY;
-      sc[4 + v] = (blk_ok && 4 + v < nvalid) ? s2[v] * qk_scale : -INFINITY;
+      sc[v] = s1[v] * qk_scale;
+      sc[4 + v] = s2[v] * qk_scale;
+    }
+    // Tiles at a sequence's end or with an invalid block are the only ones
+    // with masked tokens (a wave-uniform condition).
+    const bool partial = c0.len - 32 * c0.j < 32 || c0.blkA < 0 || c0.blkB < 0;
+    int nvalid = 8;
+    if (partial) {
+      const bool blk_ok = (lq < 2 ? c0.blkA : c0.blkB) >= 0;
+      nvalid = blk_ok ? c0.len - 32 * c0.j - 8 * lq : 0;
+#pragma unroll
+      for (int v = 0; v < 8; ++v)
+        if (v >= nvalid) sc[v] = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < NV; ++t) r0.v[t] = mask_tokens(r0.v[t], nvalid);
     }
     float mt = sc[0];
 #pragma unroll
     for (int v = 1; v < 8; ++v) mt = fmaxf(mt, sc[v]);
     mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mnew = fmaxf(m, mt);
-    const bool live = mnew != -INFINITY;
-    const float alpha = live ? __builtin_amdgcn_exp2f(m - mnew) : 1.0f;
+    // Lazy rescaling: the running max moves only when a score exceeds it by
+    // more than 8 (log2 units), so p = 2^(s - m) <= 256 -- exact enough in
+    // fp16/bf16 operands and fp32 sums -- and the O rescale is skipped on
+    // almost every tile.
+    if (__any(mt > m + 8.0f)) {
+      const float mnew = mt > m + 8.0f ? mt : m;
+      const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
+      l *= alpha;
+#pragma unroll
+      for (int t = 0; t < NV; ++t) o[t] = o[t] * alpha;
+      m = mnew;
+    }
     float pr[8];
     float psum = 0.0f;
+    const bool live = m != -INFINITY;
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      pr[v] = live ? __builtin_amdgcn_exp2f(sc[v] - mnew) : 0.0f;
+      pr[v] = live ? __builtin_amdgcn_exp2f(sc[v] - m) : 0.0f;
       psum += pr[v];
     }
-    l = l * alpha + psum;
-    m = mnew;
-    // P = P_hi + P_lo in bf16 (two MFMAs): P.V keeps ~16 mantissa bits, so
-    // rounding P costs nothing against the bf16 output rounding.
-    bf16x8_t pop, plo;
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const __bf16 hi = (__bf16)pr[v];
-      pop[v] = hi;
-      plo[v] = (__bf16)(pr[v] - (float)hi);
-    }
+    l += psum;
 
     // ---- O^T += V^T P^T --------------------------------------------------
-    const bool partial = c0.len - 32 * c0.j < 32 || c0.blkA < 0 || c0.blkB < 0;
-    const int nv_mask = blk_ok ? nvalid : 0;
+    if constexpr (KT == kE4M3) {
+      // e4m3 V converts exactly to fp16; P in fp16 (p <= 256) keeps 11 bits.
+      f16x8_t pop;
 #pragma unroll
-    for (int t = 0; t < NV; ++t) {
-      const auto raw = partial ? mask_tokens(r0.v[t], nv_mask) : r0.v[t];
-      o[t] = o[t] * alpha;
-      const bf16x8_t vop = v_operand(raw);
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, o[t], 0, 0, 0);
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo, o[t], 0, 0, 0);
+      for (int v = 0; v < 8; ++v) pop[v] = (_Float16)pr[v];
+#pragma unroll
+      for (int t = 0; t < NV; ++t)
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(e4m3x8_to_f16(r0.v[t].x, r0.v[t].y), pop, o[t], 0, 0, 0);
+    } else {
+      // bf16 V: P = P_hi + P_lo in bf16 (two MFMAs) keeps ~16 bits.
+      bf16x8_t pop, plo;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const __bf16 hi = (__bf16)pr[v];
+        pop[v] = hi;
+        plo[v] = (__bf16)(pr[v] - (float)hi);
+      }
+#pragma unroll
+      for (int t = 0; t < NV; ++t) {
+        const bf16x8_t vop = as_bf16x8(r0.v[t]);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo, o[t], 0, 0, 0);
+      }
     }
 
     // ---- end of a (sequence, head) run ------------------------------------
@@ -564,12 +605,26 @@ int cu_count() {
   return cached[dev];
 }
 
-constexpr int kStreamBlocksPerCU = 2;  // 4-wave workgroups resident per CU
+// Resident 4-wave workgroups per CU: the launch uses as many as the
+// kernel's register use allows (up to this bound, which sizes workspaces).
+constexpr int kMaxStreamBlocksPerCU = 4;
+
+template <int KT, int D>
+int blocks_per_cu() {
+  static int cached = 0;
+  if (cached == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<KT, D>, 256, 0) != hipSuccess || n < 1)
+      n = 1;
+    cached = n < kMaxStreamBlocksPerCU ? n : kMaxStreamBlocksPerCU;
+  }
+  return cached;
+}
 
 template <int KT, int D>
 int32_t launch_stream_t(const DecodeParams& p0, hipStream_t stream) {
   DecodeParams p = p0;
-  const int blocks = cu_count() * kStreamBlocksPerCU;
+  const int blocks = cu_count() * blocks_per_cu<KT, D>();
   {
     ProfileScope prof("cf_decode_mfma", stream);
     hipLaunchKernelGGL((decode_stream_kernel<KT, D>), dim3(blocks), dim3(256), 0, stream, p, p.tables, p.seq_lens,
@@ -600,7 +655,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 // Workspace layout: [o partials: 2 slots per wave x G x D f32, 256-byte
 // padded] [(m, l): 2 slots per wave x G x 2 f32].
 namespace {
-uint64_t stream_waves() { return (uint64_t)cu_count() * kStreamBlocksPerCU * 4; }
+uint64_t stream_waves() { return (uint64_t)cu_count() * kMaxStreamBlocksPerCU * 4; }
 uint64_t pad256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
 uint64_t stream_o_bytes(int64_t G, int64_t D) { return pad256(stream_waves() * 2 * G * D * 4); }
 }  // namespace
@@ -622,8 +677,9 @@ bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
   if (p.G != 1 && p.G != 2 && p.G != 4 && p.G != 8 && p.G != 16) return false;
   if (p.NB < 1) return false;  // invalid block ids are redirected to block 0 (then masked)
   const int kb = kv_dt == kE4M3 ? 1 : 2;
-  // K: channel stride 1, rows 16-byte aligned.
-  if (p.k_s[3] != 1) return false;
+  // Native layout: K tile [bs][D] (token stride D, channel stride 1), V tile
+  // [D][bs] (token stride 1, channel stride bs); block/head strides free.
+  if (p.k_s[3] != 1 || p.k_s[1] != p.D || p.v_s[1] != 1 || p.v_s[3] != 16) return false;
   for (int i = 0; i < 3; ++i)
     if ((p.k_s[i] * kb) % 16 != 0) return false;
   // V: token stride 1 (channel-major blocks), runs of 8 tokens aligned.
