@@ -188,7 +188,8 @@ int32_t cf_paged_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int6
            block_size);
   const int64_t parts = decode_max_parts(max_blocks_per_seq, block_size, partition_tokens);
   const uint64_t generic = generic_workspace_bytes(batch, num_q_heads, head_dim, parts);
-  const uint64_t mfma = block_size == 16 ? decode_mfma_workspace_bytes(num_q_heads, num_kv_heads, head_dim) : 0;
+  const uint64_t mfma =
+      block_size == 16 ? decode_mfma_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim) : 0;
   *bytes_out = generic > mfma ? generic : mfma;
   return CF_OK;
 }
@@ -280,7 +281,7 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache, const CfTens
   if (B == 0) return CF_OK;
 
   const bool mfma = decode_mfma_supported(p, vq.dtype, vk.dtype);
-  const uint64_t need = mfma ? decode_mfma_workspace_bytes(Hq, Hkv, D)
+  const uint64_t need = mfma ? decode_mfma_workspace_bytes(B, Hq, Hkv, D)
                              : generic_workspace_bytes(B, Hq, D, p.max_parts);
   if (need > 0) {
     if (workspace == nullptr || workspace_bytes < need) {

@@ -9,7 +9,7 @@
 #include <cstdio>
 #include <string>
 
-#include "../../include/cf_hip.h"
+#include "cf_hip.h"
 
 namespace cf {
 

@@ -46,6 +46,19 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// KV data is read once per call: non-temporal (streaming) loads.
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+template <class T>
+__device__ __forceinline__ T stream_load(const void* ptr);
+template <>
+__device__ __forceinline__ uint4 stream_load<uint4>(const void* ptr) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4_t*)ptr));
+}
+template <>
+__device__ __forceinline__ uint2 stream_load<uint2>(const void* ptr) {
+  return __builtin_bit_cast(uint2, __builtin_nontemporal_load((const u32x2_t*)ptr));
+}
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
 // 8 e4m3 codes (two dwords, byte order = element order) -> 8 bf16.
@@ -103,14 +116,14 @@ __device__ __forceinline__ void load_tile(TileRegs<KT, D>& r, const DecodeParams
   const uint8_t* k1 = (li < 8 ? kA : kB) + (koff * D + lq * (D / 4)) * KB;
 #pragma unroll
   for (int c = 0; c < R::KCHUNK; ++c) {
-    r.k1[c] = *(const uint4*)(k1 + 16 * c);
-    r.k2[c] = *(const uint4*)(k1 + 4 * D * KB + 16 * c);
+    r.k1[c] = stream_load<uint4>(k1 + 16 * c);
+    r.k2[c] = stream_load<uint4>(k1 + 4 * D * KB + 16 * c);
   }
   // V: lane (li, lq) reads channel 16t + li, tokens 8*(lq%2)..+7 of block A
   // (lq < 2) or B.
   const uint8_t* vp = (lq < 2 ? vA : vB) + (li * 16 + (lq & 1) * 8) * KB;
 #pragma unroll
-  for (int t = 0; t < R::NV; ++t) r.v[t] = *(const typename R::VT*)(vp + t * 256 * KB);
+  for (int t = 0; t < R::NV; ++t) r.v[t] = stream_load<typename R::VT>(vp + t * 256 * KB);
 }
 
 // Keeps the first `nbytes` bytes of an 8-byte register pair, zeroing the rest.
@@ -315,6 +328,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     if (eff_len(p, ix, bz) == 0) {
       uint16_t* orow = (uint16_t*)p.out + (int64_t)bz * p.o_sb;
       for (int e = lane; e < p.Hq * D; e += 64) orow[(int64_t)(e / D) * p.o_sh + e % D] = 0;
+      for (int hh = lane; hh < p.Hkv; hh += 64) p.merge_desc[(int64_t)bz * p.Hkv + hh] = make_int2(0, 0);
     }
   }
   const int Tb = tiles_per_head(p, ix, lane);
@@ -452,6 +466,18 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
       lt += __shfl_xor(lt, 32, 64);
       const float vs = ix.vscale ? ix.vscale[c0.h * p.vs_s] : 1.0f;
       const bool complete = run_j0 == 0 && c0.j == c0.nt - 1;
+      if (run_j0 == 0 && lane == 0) {
+        // The wave holding a sequence's first tile tells the merge kernel
+        // what to do: nothing (complete here) or which slots to combine.
+        int2 desc = make_int2(0, 0);
+        if (!complete) {
+          const int64_t s_tile = tau - c0.j;
+          const int w1 = (int)(s_tile / chunk);
+          const int w2 = (int)((s_tile + c0.nt - 1) / chunk);
+          desc = make_int2(w1 * 2 + ((int64_t)w1 * chunk < s_tile ? 1 : 0), w2 - w1 + 1);
+        }
+        p.merge_desc[(int64_t)c0.b * p.Hkv + c0.h] = desc;
+      }
       if (li < G) {
         if (complete) {
           const float inv = lt > 0.0f ? vs / lt : 0.0f;
@@ -505,26 +531,15 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p, const 
   constexpr int E = G * D / 64;  // output elements per lane
   __shared__ float wgt[64][G];
   __shared__ float inv_l[G];
-  const Index ix{nullptr, lens, nullptr, nullptr};
   const int h = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x;
-  const int nt = ntiles_of(p, ix, b);
-  if (nt == 0) return;  // zero rows come from the decode kernel
-  const int Tb = tiles_per_head(p, ix, lane);
-  int before = 0;
-  for (int base = 0; base < b; base += 64) {
-    const int bb = base + lane;
-    before += wave_sum_i(bb < b ? ntiles_of(p, ix, bb) : 0);
-  }
-  before = uniform(before);
-  const int64_t T = (int64_t)p.Hkv * Tb;
-  const int64_t chunk = (T + Wtot - 1) / Wtot;
-  const int64_t s = (int64_t)h * Tb + before, e = s + nt;
-  const int w1 = (int)(s / chunk), w2 = (int)((e - 1) / chunk);
-  if (w1 == w2) return;
-  const int nslots = w2 - w1 + 1;
-  const int slot_first = w1 * 2 + ((int64_t)w1 * chunk < s ? 1 : 0);
-
+  const int2 desc = p.merge_desc[(int64_t)b * p.Hkv + h];
+  const int nslots = desc.y;
+  if (nslots == 0) return;  // written whole by the decode kernel (or empty)
+  const int slot_first = desc.x;
+  const int w1 = slot_first >> 1;
+  (void)lens;
+  (void)Wtot;
   float acc[E];
 #pragma unroll
   for (int i = 0; i < E; ++i) acc[i] = 0.0f;
@@ -605,8 +620,12 @@ int cu_count() {
   return cached[dev];
 }
 
-// Resident 4-wave workgroups per CU: the launch uses as many as the
-// kernel's register use allows (up to this bound, which sizes workspaces).
+// Resident 4-wave workgroups per CU.  One per CU (one wave per SIMD) reads
+// the randomly placed KV blocks faster on MI355X than two or three: more
+// concurrent streams of 2 KiB chunks cost more than the latency they hide
+// (measured: 115.6 us vs 121.1 us vs 125.4 us for 1/2/3 per CU on the
+// Llama-3-8B shape).  kMaxStreamBlocksPerCU bounds workspace sizes.
+constexpr int kStreamBlocksPerCU = 1;
 constexpr int kMaxStreamBlocksPerCU = 4;
 
 template <int KT, int D>
@@ -616,7 +635,7 @@ int blocks_per_cu() {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<KT, D>, 256, 0) != hipSuccess || n < 1)
       n = 1;
-    cached = n < kMaxStreamBlocksPerCU ? n : kMaxStreamBlocksPerCU;
+    cached = n < kStreamBlocksPerCU ? n : kStreamBlocksPerCU;
   }
   return cached;
 }
@@ -653,21 +672,24 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 }  // namespace
 
 // Workspace layout: [o partials: 2 slots per wave x G x D f32, 256-byte
-// padded] [(m, l): 2 slots per wave x G x 2 f32].
+// padded] [(m, l): 2 slots per wave x G x 2 f32, padded] [merge descriptors:
+// one int2 per (sequence, KV head)].
 namespace {
 uint64_t stream_waves() { return (uint64_t)cu_count() * kMaxStreamBlocksPerCU * 4; }
 uint64_t pad256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
 uint64_t stream_o_bytes(int64_t G, int64_t D) { return pad256(stream_waves() * 2 * G * D * 4); }
+uint64_t stream_ml_bytes(int64_t G) { return pad256(stream_waves() * 2 * G * 2 * 4); }
 }  // namespace
 
-uint64_t decode_mfma_workspace_bytes(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim) {
+uint64_t decode_mfma_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim) {
   const int64_t G = num_kv_heads > 0 ? num_q_heads / num_kv_heads : num_q_heads;
-  return stream_o_bytes(G, head_dim) + stream_waves() * 2 * G * 2 * 4;
+  return stream_o_bytes(G, head_dim) + stream_ml_bytes(G) + (uint64_t)batch * num_kv_heads * 8;
 }
 
 void decode_mfma_bind_workspace(DecodeParams& p, void* workspace) {
   p.ws_o = (float*)workspace;
   p.ws_ml = (float*)((char*)workspace + stream_o_bytes(p.G, p.D));
+  p.merge_desc = (int2*)((char*)workspace + stream_o_bytes(p.G, p.D) + stream_ml_bytes(p.G));
 }
 
 bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {

@@ -25,6 +25,7 @@ struct DecodeParams {
   int64_t o_sb, o_sh;  // out [B, Hq, D], D stride 1
   float* ws_o;         // [B, Hq, max_parts, D] un-normalized partial outputs
   float* ws_ml;        // [B, Hq, max_parts, 2] running max and sum
+  int2* merge_desc;    // MFMA path: per (sequence, KV head) {first slot, slot count}
   float scale;
   int B, Hq, Hkv, G, D, bs, Mb, PT, max_parts;
   int NB;  // cache blocks; a block id outside [0, NB) contributes no tokens
@@ -35,7 +36,7 @@ int32_t launch_decode_generic(const DecodeParams& p, int q_dt, int kv_dt, hipStr
 int32_t launch_decode_mfma(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream);
 bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt);
 // Workspace of the MFMA path: two (m, l, o) partial slots per launched wave.
-uint64_t decode_mfma_workspace_bytes(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim);
+uint64_t decode_mfma_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim);
 void decode_mfma_bind_workspace(DecodeParams& p, void* workspace);
 
 int32_t launch_decode_reduce(const DecodeParams& p, int q_dt, hipStream_t stream);
