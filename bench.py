@@ -11,6 +11,11 @@ Infinity Cache does not hold the previous step's KV.
 Prints one JSON line (rank 0).  The CPU baseline is the oracle's
 restatement of the reference CPU path (gather + dequantize + SDPA) on a
 bounded sample of the same workload, timed on this host's cores.
+
+`--config c5_mixed` times BASELINE.json configs[4] instead: one mixed
+step = FP8 write of the step's 4344 new K/V rows + decode attention of 248
+sequences + chunked-prefill attention of 8 x 512-token chunks, all on one
+stream; tokens/s counts the step's new tokens (decodes + chunk rows).
 """
 
 from __future__ import annotations
@@ -27,6 +32,7 @@ sys.path.insert(0, str(ROOT / "llm-compileforge_amd"))
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFS = 2500.0
 METRIC = "paged-decode tokens/s + HBM GB/s (% peak), Llama-3-8B shape FP8 KV, 1 MI355X"
 
 
@@ -82,6 +88,90 @@ def load_traffic(config: str) -> float | None:
     return None
 
 
+def bench_mixed(args) -> dict:
+    """One c5 step per iteration: kv write + decode + chunked prefill."""
+    import torch
+
+    from cf_hip import ops, workloads
+    from kernels.paged_attention import chunked_prefill_attention
+
+    dev = torch.device("cuda:0")
+    case = workloads.make_mixed_case(args.config, device=dev, seed=0)
+    alg = workloads.mixed_algorithmic(case)
+    pools = [workloads.materialize_mixed(case, args.layout) for _ in range(args.pools)]
+    steps_fns = []
+    for t in pools:
+        plan = ops.DecodePlan(t["q_decode"], t["k_cache"], t["v_cache"], t["decode_tables"], t["decode_lens"],
+                              case.scale, case.block_size, t["k_scale"], t["v_scale"], args.partition)
+        ws = ops.new_workspace(ops.prefill_workspace_bytes(case.q_prefill.shape[0], len(case.prefill_lens),
+                                                           case.q_prefill.shape[1], case.num_kv_heads,
+                                                           case.q_prefill.shape[2]), dev)
+        out_p = torch.empty_like(t["q_prefill"])
+
+        def step(t=t, plan=plan, ws=ws, out_p=out_p):
+            ops.kv_write_fp8(t["k_new"], t["v_new"], t["slots"], t["k_cache"], t["v_cache"], t["k_scale"],
+                             t["v_scale"])
+            plan.run()
+            chunked_prefill_attention(t["q_prefill"], t["k_cache"], t["v_cache"], t["prefill_tables"],
+                                      t["prefill_lens"], t["q_start"], case.block_size, case.scale,
+                                      k_scale=t["k_scale"], v_scale=t["v_scale"], out=out_p, workspace=ws)
+
+        steps_fns.append(step)
+    torch.cuda.synchronize()
+    log(f"c5: {alg['decode_tokens']} decodes, {alg['prefill_tokens']} chunk rows; decode bytes "
+        f"{alg['decode_bytes'] / 1e9:.2f} GB, prefill {alg['prefill_flops'] / 1e9:.1f} GFLOP")
+    for i in range(args.warmup):
+        steps_fns[i % len(steps_fns)]()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        steps_fns[i % len(steps_fns)]()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    with ops.KernelTimer() as timer:
+        for i in range(args.steps):
+            steps_fns[i % len(steps_fns)]()
+        torch.cuda.synchronize()
+    us = {}
+    for name in ("cf_kv_write_fp8", "cf_decode_mfma", "cf_decode_merge", "cf_prefill_plan", "cf_prefill_mfma",
+                 "cf_prefill_merge"):
+        ms, n = timer.query(name)
+        us[name] = ms / max(n, 1) * 1e3
+    timer.reset()
+    log(f"{ms_step * 1e3:.1f} us/step; " + ", ".join(f"{k} {v:.1f} us" for k, v in us.items()))
+    dec_s = us["cf_decode_mfma"] / 1e6
+    pre_s = us["cf_prefill_mfma"] / 1e6
+    dec_gbs = alg["decode_bytes"] / dec_s / 1e9
+    pre_tf = alg["prefill_flops"] / pre_s / 1e12
+    tokens = alg["decode_tokens"] + alg["prefill_tokens"]
+    return {
+        "metric": "mixed chunked-prefill + decode step tokens/s, Llama-3-8B shape FP8 KV, 1 MI355X",
+        "value": tokens / (ms_step / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3 KV / bf16 q / f32 accumulate",
+        "data": "synthetic (seeded), random-init",
+        "config": {"workload": args.config, "decodes": alg["decode_tokens"], "chunk_rows": alg["prefill_tokens"],
+                   "chunks": len(case.prefill_lens), "num_q_heads": case.q_prefill.shape[1],
+                   "num_kv_heads": case.num_kv_heads, "head_dim": case.q_prefill.shape[2],
+                   "block_size": case.block_size, "kv_layout": args.layout, "cache_pools_rotated": args.pools,
+                   "parallelism": "single GPU"},
+        "kernel_us": us,
+        "algorithmic": alg,
+        "roofline": {"bound": "hbm", "kernel": "cf_decode_mfma", "achieved": dec_gbs, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": dec_gbs / HBM_PEAK_GBS, "traffic": None},
+        "roofline_prefill": {"bound": "mfma", "kernel": "cf_prefill_mfma", "achieved": pre_tf,
+                             "peak": BF16_MFMA_PEAK_TFS, "unit": "TFLOP/s", "frac": pre_tf / BF16_MFMA_PEAK_TFS,
+                             "traffic": None},
+    }
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,6 +198,10 @@ def main() -> None:
 
     dev = torch.device("cuda:0")
     log(f"device {torch.cuda.get_device_name(dev)}; building {args.config}")
+    if args.config == "c5_mixed":
+        result = bench_mixed(args)
+        print(json.dumps(result), flush=True)
+        return
     case = workloads.make_case(args.config, device=dev, seed=0, batch=args.batch)
     pools = []
     for i in range(args.pools):

@@ -120,6 +120,48 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache,
                         CfTensor* out, void* workspace,
                         uint64_t workspace_bytes, void* stream);
 
+/* Workspace needed by cf_prefill_chunk_fp8 (on the current device) for
+ * num_q_tokens query rows in num_chunks chunks.  Grows with the query
+ * rows (one small record per query block), not with the cached context. */
+int32_t cf_prefill_chunk_workspace_bytes(int64_t num_q_tokens, int64_t num_chunks,
+                                         int64_t num_q_heads, int64_t num_kv_heads,
+                                         int64_t head_dim, int32_t block_size,
+                                         uint64_t* bytes_out);
+
+/* Chunked-prefill attention over the paged cache: the chunk step of the
+ * reference's scheduler (runtime/src/engine/scheduler.rs:178-226), whose
+ * attention the reference states only as the per-row decode of
+ * kernels/paged_attention.py:21-73 with the length cut to the row, and
+ * dense causal attention (kernels/flash_attention.py:179-202) when nothing
+ * is cached.  The chunk's own K/V are in the cache already
+ * (cf_kv_write_fp8).
+ *
+ *   q            [Tq, Hq, D]           bf16, D stride 1, rows of all chunks
+ *   k_cache,     [NB, 16, Hkv, D]      bf16 | e4m3fn, native layout (as the
+ *   v_cache                            MFMA decode path)
+ *   block_tables [N, Mb]               i32, one row per chunk's sequence
+ *   seq_lens     [N]                   i32, tokens of the sequence including
+ *                                      the chunk
+ *   q_start      [N + 1]               i32, chunk n owns q rows
+ *                                      [q_start[n], q_start[n+1])
+ *   k_scale, v_scale                   as cf_paged_decode
+ *   out          [Tq, Hq, D]           bf16
+ *
+ * Chunk n has L = q_start[n+1] - q_start[n] rows; row i sits at position
+ * seq_lens[n] - L + i and attends to cache positions [0, that] (causal:
+ * bottom-right aligned), read through block_tables[n] up to Mb*16 tokens.
+ * Chunks are taken in order and made disjoint (a chunk starting before the
+ * previous one ends starts where it ends).  Rows at negative positions get
+ * zeros; rows outside every chunk are not written.  block_size must be 16.
+ * Unsupported dtypes/layouts return CF_ERR_UNSUPPORTED (no generic path).
+ * workspace: cf_prefill_chunk_workspace_bytes() bytes, 256-byte aligned. */
+int32_t cf_prefill_chunk_fp8(const CfTensor* q, const CfTensor* k_cache,
+                             const CfTensor* v_cache, const CfTensor* block_tables,
+                             const CfTensor* seq_lens, const CfTensor* q_start,
+                             const CfTensor* k_scale, const CfTensor* v_scale,
+                             float scale, int32_t block_size, CfTensor* out,
+                             void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Per-head FP8 scale: scales[h] = amax/448 over x[:, h, :], clamped below
  * at 1e-12, and 1.0 where amax == 0.  This is
  * FP8KVCacheQuantizer.quantize_block's scale rule (reference

@@ -140,6 +140,16 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _P, _P, _P, _P, _P, _P, ctypes.c_float, ctypes.c_int32, ctypes.c_int32, _P, ctypes.c_void_p,
          ctypes.c_uint64, ctypes.c_void_p],
     ),
+    "cf_prefill_chunk_workspace_bytes": (
+        ctypes.c_int32,
+        [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+         ctypes.POINTER(ctypes.c_uint64)],
+    ),
+    "cf_prefill_chunk_fp8": (
+        ctypes.c_int32,
+        [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_float, ctypes.c_int32, _P, ctypes.c_void_p, ctypes.c_uint64,
+         ctypes.c_void_p],
+    ),
     "cf_fp8_amax_scale": (ctypes.c_int32, [_P, _P, ctypes.c_void_p]),
     "cf_fp8_quantize": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
     "cf_fp8_dequantize": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),

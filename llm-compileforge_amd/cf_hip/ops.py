@@ -117,6 +117,64 @@ def paged_decode(
     return out
 
 
+def prefill_workspace_bytes(num_q_tokens: int, num_chunks: int, num_q_heads: int, num_kv_heads: int,
+                            head_dim: int, block_size: int = 16) -> int:
+    out = ctypes.c_uint64(0)
+    rc = lib().cf_prefill_chunk_workspace_bytes(
+        num_q_tokens, num_chunks, num_q_heads, num_kv_heads, head_dim, block_size, ctypes.byref(out)
+    )
+    check(rc, "cf_prefill_chunk_workspace_bytes")
+    return int(out.value)
+
+
+def prefill_chunk(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    q_start: torch.Tensor,
+    scale: float,
+    block_size: int = 16,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Chunked-prefill attention over the paged cache; returns out [Tq, Hq, D].
+
+    q [Tq, Hq, D] bf16 holds the rows of N chunks, chunk n owning rows
+    [q_start[n], q_start[n+1]); block_tables int32 [N, Mb]; seq_lens int32
+    [N] counts the sequence's tokens including the chunk (already written
+    to the cache).  Row i of a chunk of L rows attends causally to cache
+    positions [0, seq_lens[n] - L + i].  Caches: bf16 or e4m3fn in the
+    native layout, block_size 16.
+    """
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("block_tables", block_tables),
+                    ("seq_lens", seq_lens), ("q_start", q_start)):
+        _require_device(name, t)
+    dev = _same_device(q, k_cache, v_cache, block_tables, seq_lens, q_start)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=dev)
+    need = prefill_workspace_bytes(q.shape[0], block_tables.shape[0], q.shape[1], k_cache.shape[2], q.shape[2],
+                                   block_size)
+    if workspace is None:
+        workspace = _cached_workspace(need, dev)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace of {need} bytes needed, {workspace.numel() * workspace.element_size()} given")
+    ks = descriptor(k_scale) if k_scale is not None else None
+    vs = descriptor(v_scale) if v_scale is not None else None
+    d = [descriptor(t) for t in (q, k_cache, v_cache, block_tables, seq_lens, q_start)]
+    do = descriptor(out)
+    with torch.cuda.device(dev):
+        rc = lib().cf_prefill_chunk_fp8(
+            *(ref(x) for x in d), ref(ks), ref(vs), float(scale), int(block_size), ref(do),
+            workspace.data_ptr(), need, stream_handle(dev),
+        )
+    check(rc, "cf_prefill_chunk_fp8")
+    return out
+
+
 class DecodePlan:
     """A paged decode call with its descriptors built once.
 
@@ -271,6 +329,8 @@ __all__ = [
     "DecodePlan",
     "KernelTimer",
     "decode_workspace_bytes",
+    "prefill_chunk",
+    "prefill_workspace_bytes",
     "new_workspace",
     "fp8_amax_scale",
     "fp8_dequantize",

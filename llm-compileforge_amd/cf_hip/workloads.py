@@ -18,6 +18,15 @@ Configs (names used by bench.py and the tests):
   c4_llama3_70b B=128, Hq=64/Hkv=8, D=128, e4m3, ctx = round(lognormal(
                 ln 4096, sigma=1)) clipped to [512, 32768].
 All use block_size 16 and softmax scale 1/sqrt(D).
+
+  c5_mixed      one mixed chunked-prefill + decode step at the c3 shape
+                (Hq=32/Hkv=8, D=128, e4m3): 8 chunks of 512 new tokens with
+                a cached prefix of U{0..4096} tokens, plus 248 decodes with
+                ctx U{512..8192}.  The 8*512 + 248 new K/V rows (bf16
+                N(0,1)) are written into the cache in the step, quantized
+                with per-KV-head scales calibrated over the pool and the new
+                rows (amax/448); then decode and prefill attention read the
+                FP8 cache.  Built by make_mixed_case.
 """
 
 from __future__ import annotations
@@ -72,6 +81,8 @@ def _ctx_uniform(gen: torch.Generator, b: int, lo: int, hi: int) -> list[int]:
 
 
 def _randn(shape: tuple[int, ...], dtype: torch.dtype, device: torch.device, seed: int) -> torch.Tensor:
+    if device.type == "meta":  # shapes only (tables, lengths and slots are still sampled)
+        return torch.empty(shape, dtype=dtype, device=device)
     g = torch.Generator(device=device)
     g.manual_seed(seed)
     return torch.randn(shape, generator=g, device=device, dtype=torch.float32).to(dtype)
@@ -216,3 +227,155 @@ def algorithmic_bytes(case: DecodeCase) -> dict[str, int]:
         "unique_kv": unique_tokens * per_tok,
         "tokens": logical_tokens,
     }
+
+
+@dataclass
+class MixedCase:
+    """One chunked-prefill + decode step (see c5_mixed)."""
+
+    name: str
+    k_pool: torch.Tensor  # logical [NB, bs, Hkv, D] cache contents before the step (source dtype)
+    v_pool: torch.Tensor
+    k_new: torch.Tensor  # [T_new, Hkv, D]: chunk rows in q order, then one row per decode
+    v_new: torch.Tensor
+    slots: list[int]  # cache slot (block * bs + offset) of each new row
+    q_prefill: torch.Tensor  # [Tq, Hq, D]
+    q_decode: torch.Tensor  # [Bd, Hq, D]
+    prefill_tables: list[list[int]]
+    prefill_lens: list[int]  # cached + chunk tokens
+    q_start: list[int]  # [N + 1]
+    decode_tables: list[list[int]]
+    decode_lens: list[int]
+    block_size: int
+    scale: float
+    kv_dtype: torch.dtype
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def num_kv_heads(self) -> int:
+        return self.k_pool.shape[2]
+
+
+def make_mixed_case(
+    config: str = "c5_mixed",
+    device: torch.device | str = "cpu",
+    seed: int = 0,
+    *,
+    chunks: list[int] | None = None,
+    cached: list[int] | None = None,
+    decode_lens: list[int] | None = None,
+    num_q_heads: int = 32,
+    num_kv_heads: int = 8,
+    head_dim: int = 128,
+    kv_dtype: torch.dtype = torch.float8_e4m3fn,
+) -> MixedCase:
+    """Builds c5_mixed, or the same step with other chunk lengths, cached
+    prefixes, decode lengths or head shape (explicit lists override the
+    sampled ones)."""
+    if config != "c5_mixed":
+        raise ValueError(f"unknown mixed config {config!r}")
+    device = torch.device(device)
+    gen = torch.Generator().manual_seed(seed)
+    bs = 16
+    if chunks is None:
+        chunks = [512] * 8
+    if cached is None:
+        cached = _ctx_uniform(gen, len(chunks), 0, 4096)
+    if decode_lens is None:
+        decode_lens = _ctx_uniform(gen, 248, 512, 8192)
+    if len(cached) != len(chunks):
+        raise ValueError("chunks and cached must have the same length")
+    prefill_lens = [c + n for c, n in zip(cached, chunks)]
+    lens = prefill_lens + list(decode_lens)
+    nb = sum((n + bs - 1) // bs for n in lens) + 16
+    perm = torch.randperm(nb, generator=gen).tolist()
+    tables = _tables_from_perm(perm, lens, bs)
+    ptables, dtables = tables[: len(chunks)], tables[len(chunks):]
+    slots: list[int] = []
+    for t, c, n in zip(ptables, cached, chunks):
+        slots += [t[p // bs] * bs + p % bs for p in range(c, c + n)]
+    for t, n in zip(dtables, decode_lens):
+        slots.append(t[(n - 1) // bs] * bs + (n - 1) % bs)
+    q_start = [0]
+    for n in chunks:
+        q_start.append(q_start[-1] + n)
+    hq, hkv, d = num_q_heads, num_kv_heads, head_dim
+    src = torch.bfloat16
+    k_pool = _randn((nb, bs, hkv, d), src, device, seed + 2)
+    v_pool = _randn((nb, bs, hkv, d), src, device, seed + 3)
+    k_new = _randn((len(slots), hkv, d), src, device, seed + 4)
+    v_new = _randn((len(slots), hkv, d), src, device, seed + 5)
+    q_prefill = _randn((q_start[-1], hq, d), torch.bfloat16, device, seed + 6)
+    q_decode = _randn((len(decode_lens), hq, d), torch.bfloat16, device, seed + 7)
+    return MixedCase(config, k_pool, v_pool, k_new, v_new, slots, q_prefill, q_decode, ptables, prefill_lens,
+                     q_start, dtables, list(decode_lens), bs, 1.0 / math.sqrt(d), kv_dtype,
+                     {"cached": list(cached), "chunks": list(chunks)})
+
+
+def _int_tensor(rows: list[list[int]], device) -> torch.Tensor:
+    mb = max([1] + [len(t) for t in rows])
+    out = torch.zeros(len(rows), mb, dtype=torch.int32)
+    for i, t in enumerate(rows):
+        if t:
+            out[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    return out.to(device)
+
+
+def materialize_mixed(case: MixedCase, layout: str = "native") -> dict[str, torch.Tensor | None]:
+    """Device tensors of the step: the cache before the step (e4m3 with
+    scales calibrated over pool and new rows, or bf16) and every input of
+    the write, decode and prefill calls."""
+    from . import ops
+
+    dev = case.k_pool.device
+    nb, bs, hkv, d = case.k_pool.shape
+    t: dict[str, torch.Tensor | None] = {}
+    if case.kv_dtype == torch.float8_e4m3fn:
+        ks = torch.maximum(ops.fp8_amax_scale(case.k_pool), ops.fp8_amax_scale(case.k_new))
+        vs = torch.maximum(ops.fp8_amax_scale(case.v_pool), ops.fp8_amax_scale(case.v_new))
+        kc, vc = _layout.alloc_kv_cache(nb, bs, hkv, d, torch.float8_e4m3fn, dev, layout)
+        ops.fp8_quantize(case.k_pool, ks, out=kc)
+        ops.fp8_quantize(case.v_pool, vs, out=vc)
+        t.update(k_scale=ks, v_scale=vs)
+    else:
+        kc, vc = _layout.alloc_kv_cache(nb, bs, hkv, d, case.kv_dtype, dev, layout)
+        kc.copy_(case.k_pool)
+        vc.copy_(case.v_pool)
+        t.update(k_scale=None, v_scale=None)
+    t.update(
+        k_cache=kc, v_cache=vc,
+        k_new=case.k_new, v_new=case.v_new,
+        slots=torch.tensor(case.slots, dtype=torch.int64).to(dev),
+        q_prefill=case.q_prefill, q_decode=case.q_decode,
+        prefill_tables=_int_tensor(case.prefill_tables, dev),
+        prefill_lens=torch.tensor(case.prefill_lens, dtype=torch.int32).to(dev),
+        q_start=torch.tensor(case.q_start, dtype=torch.int32).to(dev),
+        decode_tables=_int_tensor(case.decode_tables, dev),
+        decode_lens=torch.tensor(case.decode_lens, dtype=torch.int32).to(dev),
+    )
+    return t
+
+
+def mixed_algorithmic(case: MixedCase) -> dict[str, float]:
+    """Minimum bytes and flops of the step's parts.
+
+    write: new rows read (source dtype) + codes written; decode: KV bytes of
+    every decode's context + q/o; prefill: KV bytes of each chunk's
+    sequence (read once) + q/o, and the QK^T + PV flops of the causal rows
+    (4 * D flops per (row, query head, attended token))."""
+    esize = torch.tensor([], dtype=case.kv_dtype).element_size()
+    hkv, d = case.num_kv_heads, case.k_pool.shape[3]
+    hq = case.q_prefill.shape[1]
+    per_tok = 2 * hkv * d * esize
+    t_new = len(case.slots)
+    write = 2 * t_new * hkv * d * (case.k_new.element_size() + esize)
+    qo_d = 2 * case.q_decode.numel() * 2
+    decode = sum(case.decode_lens) * per_tok + qo_d
+    qo_p = 2 * case.q_prefill.numel() * 2
+    prefill = sum(case.prefill_lens) * per_tok + qo_p
+    attended = 0
+    for (c, n) in zip(case.meta["cached"], case.meta["chunks"]):
+        attended += n * c + n * (n + 1) // 2
+    flops = 4.0 * d * hq * attended
+    return {"write_bytes": write, "decode_bytes": decode, "prefill_bytes": prefill, "prefill_flops": flops,
+            "decode_tokens": len(case.decode_lens), "prefill_tokens": t_new - len(case.decode_lens)}

@@ -13,6 +13,7 @@
 #include "cf_host.hpp"
 #include "decode_params.hpp"
 #include "kv_fp8.hpp"
+#include "prefill_params.hpp"
 
 namespace cf {
 
@@ -306,6 +307,125 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache, const CfTens
   if (rc) return rc;
   if (p.max_parts > 1) rc = launch_decode_reduce(p, vq.dtype, st);
   return rc;
+}
+
+int32_t cf_prefill_chunk_workspace_bytes(int64_t num_q_tokens, int64_t num_chunks, int64_t num_q_heads,
+                                         int64_t num_kv_heads, int64_t head_dim, int32_t block_size,
+                                         uint64_t* bytes_out) {
+  CF_CHECK(bytes_out != nullptr, "bytes_out is NULL");
+  CF_CHECK(num_q_tokens >= 0 && num_chunks >= 0 && num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0,
+           "invalid sizes");
+  CF_CHECK(num_q_heads % num_kv_heads == 0, "num_heads %lld is not a multiple of num_kv_heads %lld",
+           (long long)num_q_heads, (long long)num_kv_heads);
+  CF_CHECK(block_size == 16, "block_size must be 16, got %d", block_size);
+  *bytes_out = prefill_workspace_bytes(num_q_tokens, num_chunks, num_q_heads, num_kv_heads, head_dim);
+  return CF_OK;
+}
+
+int32_t cf_prefill_chunk_fp8(const CfTensor* q, const CfTensor* k_cache, const CfTensor* v_cache,
+                             const CfTensor* block_tables, const CfTensor* seq_lens, const CfTensor* q_start,
+                             const CfTensor* k_scale, const CfTensor* v_scale, float scale, int32_t block_size,
+                             CfTensor* out, void* workspace, uint64_t workspace_bytes, void* stream) {
+  View vq, vk, vv, vt, vs, vqs, vo;
+  int32_t rc;
+  if ((rc = view_of(q, "q", 3, &vq))) return rc;
+  if ((rc = view_of(k_cache, "k_cache", 4, &vk))) return rc;
+  if ((rc = view_of(v_cache, "v_cache", 4, &vv))) return rc;
+  if ((rc = view_of(block_tables, "block_tables", 2, &vt))) return rc;
+  if ((rc = view_of(seq_lens, "seq_lens", 1, &vs))) return rc;
+  if ((rc = view_of(q_start, "q_start", 1, &vqs))) return rc;
+  if ((rc = view_of(out, "out", 3, &vo))) return rc;
+
+  CF_CHECK(vq.dtype == CF_BF16, "q: dtype must be bf16, got %s", dtype_name(vq.dtype));
+  CF_CHECK(vk.dtype == CF_BF16 || vk.dtype == CF_F8E4M3FN, "k_cache: dtype must be bf16 or f8e4m3fn, got %s",
+           dtype_name(vk.dtype));
+  CF_CHECK(vv.dtype == vk.dtype, "v_cache dtype %s differs from k_cache dtype %s", dtype_name(vv.dtype),
+           dtype_name(vk.dtype));
+  CF_CHECK(vt.dtype == CF_I32, "block_tables: expected i32, got %s", dtype_name(vt.dtype));
+  CF_CHECK(vs.dtype == CF_I32, "seq_lens: expected i32, got %s", dtype_name(vs.dtype));
+  CF_CHECK(vqs.dtype == CF_I32, "q_start: expected i32, got %s", dtype_name(vqs.dtype));
+  CF_CHECK(vo.dtype == CF_BF16, "out: dtype must be bf16, got %s", dtype_name(vo.dtype));
+
+  const int64_t Tq = vq.size[0], Hq = vq.size[1], D = vq.size[2];
+  const int64_t NB = vk.size[0], bs = vk.size[1], Hkv = vk.size[2];
+  const int64_t N = vt.size[0];
+  for (int i = 0; i < 4; ++i)
+    CF_CHECK(vv.size[i] == vk.size[i], "v_cache shape differs from k_cache shape on dim %d", i);
+  CF_CHECK(vk.size[3] == D, "k_cache head_dim %lld differs from q head_dim %lld", (long long)vk.size[3],
+           (long long)D);
+  CF_CHECK(block_size == 16, "block_size must be 16, got %d", block_size);
+  CF_CHECK(bs == block_size, "k_cache block dim %lld differs from block_size %d", (long long)bs, block_size);
+  CF_CHECK(Hq > 0, "q has no heads");
+  CF_CHECK(Hkv > 0 && Hq % Hkv == 0, "num_heads %lld is not a multiple of num_kv_heads %lld", (long long)Hq,
+           (long long)Hkv);
+  CF_CHECK(vs.size[0] == N, "seq_lens has %lld entries, block_tables has %lld rows", (long long)vs.size[0],
+           (long long)N);
+  CF_CHECK(vqs.size[0] == N + 1, "q_start must have %lld entries, got %lld", (long long)(N + 1),
+           (long long)vqs.size[0]);
+  CF_CHECK(vo.size[0] == Tq && vo.size[1] == Hq && vo.size[2] == D, "out shape must be [%lld, %lld, %lld]",
+           (long long)Tq, (long long)Hq, (long long)D);
+  CF_CHECK(vq.stride[2] == 1, "q: head_dim stride must be 1");
+  CF_CHECK(vo.stride[2] == 1, "out: head_dim stride must be 1");
+  CF_CHECK(NB < (int64_t)INT32_MAX, "too many cache blocks");
+  CF_CHECK(Tq < (int64_t)INT32_MAX / 2 && N < (int64_t)INT32_MAX / 2, "too many query rows or chunks");
+  CF_CHECK(Hkv < 65536, "too many KV heads");
+  CF_CHECK(std::isfinite(scale), "scale must be finite");
+
+  PrefillParams p{};
+  p.q = vq.base;
+  p.q_sr = vq.stride[0];
+  p.q_sh = vq.stride[1];
+  p.out = vo.base;
+  p.o_sr = vo.stride[0];
+  p.o_sh = vo.stride[1];
+  p.k = vk.base;
+  p.v = vv.base;
+  for (int i = 0; i < 4; ++i) {
+    p.k_s[i] = vk.stride[i];
+    p.v_s[i] = vv.stride[i];
+  }
+  p.tables = (const int32_t*)vt.base;
+  p.t_sb = vt.stride[0];
+  p.t_sm = vt.stride[1];
+  p.seq_lens = (const int32_t*)vs.base;
+  p.sl_s = vs.stride[0];
+  p.q_start = (const int32_t*)vqs.base;
+  p.qs_s = vqs.stride[0];
+  p.scale = scale;
+  p.N = (int)N;
+  p.Tq = (int)Tq;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.G = (int)(Hq / Hkv);
+  p.D = (int)D;
+  p.Mb = (int)vt.size[1];
+  p.NB = (int)NB;
+  if (vk.dtype == CF_F8E4M3FN) {
+    CF_CHECK(k_scale != nullptr && v_scale != nullptr, "f8e4m3fn caches need k_scale and v_scale");
+    if ((rc = scale_view(k_scale, "k_scale", Hkv, &p.k_scale, &p.ks_s))) return rc;
+    if ((rc = scale_view(v_scale, "v_scale", Hkv, &p.v_scale, &p.vs_s))) return rc;
+  } else {
+    CF_CHECK(k_scale == nullptr && v_scale == nullptr, "k_scale/v_scale apply to f8e4m3fn caches only");
+  }
+  if (!prefill_supported(p, vq.dtype, vk.dtype)) {
+    set_error("prefill: needs head_dim 64/128, GQA group 1/2/4/8/16, native-layout caches with 16-byte "
+              "aligned blocks and heads, and 16-byte aligned q rows");
+    return CF_ERR_UNSUPPORTED;
+  }
+  if (Tq == 0 || N == 0) return CF_OK;
+  p.QB = prefill_query_block(p.G);
+  p.max_v = (int)(Tq / p.QB + N + 1);
+  CF_CHECK(((int64_t)p.max_v + 1) * ceil_div(vt.size[1] * 16, 32) < (int64_t)INT32_MAX,
+           "query blocks x context tiles overflow int32");
+  const uint64_t need = prefill_workspace_bytes(Tq, N, Hq, Hkv, D);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("workspace of %llu bytes needed, %llu given", (unsigned long long)need,
+              (unsigned long long)workspace_bytes);
+    return CF_ERR_WORKSPACE;
+  }
+  CF_CHECK(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
+  prefill_bind_workspace(p, workspace);
+  return launch_prefill(p, vk.dtype, as_stream(stream));
 }
 
 int32_t cf_fp8_amax_scale(const CfTensor* x, CfTensor* scales, void* stream) {

@@ -30,143 +30,14 @@
 // 1.0); the per-KV-head dequant scales factor out of both products.
 // Workgroups combine their waves through LDS and write either the final
 // output (one partition) or (m, l, o) partials for decode_reduce.
-#include <type_traits>
-
 #include "cf_device.hpp"
 #include "cf_host.hpp"
 #include "decode_params.hpp"
+#include "mfma_tile.hpp"
 
 namespace cf {
 
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-constexpr float kLog2e = 1.4426950408889634f;
-
-// KV data is read once per call: non-temporal (streaming) loads.
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
-template <class T>
-__device__ __forceinline__ T stream_load(const void* ptr);
-template <>
-__device__ __forceinline__ uint4 stream_load<uint4>(const void* ptr) {
-  return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4_t*)ptr));
-}
-template <>
-__device__ __forceinline__ uint2 stream_load<uint2>(const void* ptr) {
-  return __builtin_bit_cast(uint2, __builtin_nontemporal_load((const u32x2_t*)ptr));
-}
-__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
-
-// 8 e4m3 codes (two dwords, byte order = element order) -> 8 bf16.
-__device__ __forceinline__ bf16x8_t e4m3x8_to_bf16(uint32_t lo, uint32_t hi) {
-  uint4 r;
-  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
-  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
-  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
-  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
-  return as_bf16x8(r);
-}
-
-template <int KT>
-struct KvTraits;
-template <>
-struct KvTraits<kE4M3> {
-  static constexpr int kBytes = 1;
-};
-template <>
-struct KvTraits<kBF16> {
-  static constexpr int kBytes = 2;
-};
-
-// Raw per-lane registers of one 32-token tile.
-template <int KT, int D>
-struct TileRegs {
-  static constexpr int KB = KvTraits<KT>::kBytes;
-  static constexpr int KCHUNK = D / 4 * KB / 16;  // uint4 per K row slice
-  static constexpr int NV = D / 16;
-  uint4 k1[KCHUNK];  // K row slice of token 8*(i/4) + i%4
-  uint4 k2[KCHUNK];  // ... and of that token + 4
-  // V: 8 tokens of one channel per PV MFMA (8 bytes e4m3, 16 bytes bf16)
-  using VT = typename std::conditional<KB == 1, uint2, uint4>::type;
-  VT v[NV];
-};
-
-// Loads one 32-token tile (blocks blkA, blkB of KV head h) in the native
-// layout: K tile [bs][D] (token rows), V tile [D][bs] (channel rows), each
-// (block, head) tile contiguous.  Inner offsets are compile-time constants
-// (immediate offsets of the loads); block/head strides are uniform.
-// Invalid blocks (id -1) read block 0 instead; their tokens are masked.
-template <int KT, int D>
-__device__ __forceinline__ void load_tile(TileRegs<KT, D>& r, const DecodeParams& p, const uint8_t* kbase,
-                                          const uint8_t* vbase, int blkA, int blkB, int li, int lq, int h) {
-  constexpr int KB = KvTraits<KT>::kBytes;
-  using R = TileRegs<KT, D>;
-  const int64_t a = blkA < 0 ? 0 : blkA, bb = blkB < 0 ? 0 : blkB;
-  const uint8_t* kA = kbase + (a * p.k_s[0] + (int64_t)h * p.k_s[2]) * KB;
-  const uint8_t* kB = kbase + (bb * p.k_s[0] + (int64_t)h * p.k_s[2]) * KB;
-  const uint8_t* vA = vbase + (a * p.v_s[0] + (int64_t)h * p.v_s[2]) * KB;
-  const uint8_t* vB = vbase + (bb * p.v_s[0] + (int64_t)h * p.v_s[2]) * KB;
-  // K: lane (li, lq) reads token koff = 8*(li/4)%16 + li%4 (+4) of block A
-  // (li < 8) or B, channels [lq*D/4, (lq+1)*D/4).
-  const int koff = (8 * (li >> 2) + (li & 3)) & 15;
-  const uint8_t* k1 = (li < 8 ? kA : kB) + (koff * D + lq * (D / 4)) * KB;
-#pragma unroll
-  for (int c = 0; c < R::KCHUNK; ++c) {
-    r.k1[c] = stream_load<uint4>(k1 + 16 * c);
-    r.k2[c] = stream_load<uint4>(k1 + 4 * D * KB + 16 * c);
-  }
-  // V: lane (li, lq) reads channel 16t + li, tokens 8*(lq%2)..+7 of block A
-  // (lq < 2) or B.
-  const uint8_t* vp = (lq < 2 ? vA : vB) + (li * 16 + (lq & 1) * 8) * KB;
-#pragma unroll
-  for (int t = 0; t < R::NV; ++t) r.v[t] = stream_load<typename R::VT>(vp + t * 256 * KB);
-}
-
-// Keeps the first `nbytes` bytes of an 8-byte register pair, zeroing the rest.
-__device__ __forceinline__ uint2 keep_bytes(uint2 v, int nbytes) {
-  const uint64_t x = ((uint64_t)v.y << 32) | v.x;
-  const uint64_t m = nbytes >= 8 ? ~0ull : (nbytes <= 0 ? 0ull : ((1ull << (8 * nbytes)) - 1));
-  const uint64_t y = x & m;
-  return make_uint2((uint32_t)y, (uint32_t)(y >> 32));
-}
-
-// Zeroes the V elements of this lane's tokens >= n_valid (of its 8): cache
-// slots past a sequence's end may hold any bit pattern, NaN codes included,
-// and 0 * NaN would poison the sum.
-__device__ __forceinline__ uint2 mask_tokens(uint2 v, int n_valid) { return keep_bytes(v, n_valid); }
-__device__ __forceinline__ uint4 mask_tokens(uint4 v, int n_valid) {
-  const uint2 lo = keep_bytes(make_uint2(v.x, v.y), n_valid * 2);
-  const uint2 hi = keep_bytes(make_uint2(v.z, v.w), n_valid * 2 - 8);
-  return make_uint4(lo.x, lo.y, hi.x, hi.y);
-}
-
-template <int KT>
-__device__ __forceinline__ bf16x8_t k_operand(const uint4* raw, int c) {
-  if constexpr (KT == kE4M3) {
-    const uint4 u = raw[c >> 1];
-    return (c & 1) ? e4m3x8_to_bf16(u.z, u.w) : e4m3x8_to_bf16(u.x, u.y);
-  } else {
-    return as_bf16x8(raw[c]);
-  }
-}
-
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-
-// 8 e4m3 codes -> 8 fp16 (exact: e4m3 values lie inside fp16's range and
-// precision).
-__device__ __forceinline__ f16x8_t e4m3x8_to_f16(uint32_t lo, uint32_t hi) {
-  uint4 r;
-  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false));
-  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true));
-  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false));
-  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true));
-  return __builtin_bit_cast(f16x8_t, r);
-}
-
 
 // ---------------------------------------------------------------------------
 // Work split: the "tile stream".
@@ -209,22 +80,8 @@ __device__ __forceinline__ int ntiles_of(const DecodeParams& p, const Index& ix,
   return (eff_len(p, ix, b) + 31) >> 5;
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(v, o, 64);
-    if (lane >= o) v += u;
-  }
-  return v;
-}
 
-__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Tiles per KV head (sum over sequences).
 __device__ int tiles_per_head(const DecodeParams& p, const Index& ix, int lane) {
@@ -354,10 +211,9 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   bool has1 = tau + 1 < tau_end;
   if (has1) c1 = advance(p, ix, c0);
 
-  const uint8_t* kbase = (const uint8_t*)p.k;
-  const uint8_t* vbase = (const uint8_t*)p.v;
+  const KvCacheView kv{(const uint8_t*)p.k, (const uint8_t*)p.v, p.k_s[0], p.k_s[2], p.v_s[0], p.v_s[2]};
   TileRegs<KT, D> r0, r1;
-  load_tile<KT, D>(r0, p, kbase, vbase, c0.blkA, c0.blkB, li, lq, c0.h);
+  load_tile<KT, D>(r0, kv, c0.blkA, c0.blkB, li, lq, c0.h);
 
   bf16x8_t qop[NC];
   load_q<D>(qop, p, c0.b, c0.h, li, lq);
@@ -372,7 +228,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     // Always issue the next tile's loads (the last iteration reloads its
     // own tile) so every path has the same number of loads in flight and
     // the compiler's vmcnt waits stay exact.
-    load_tile<KT, D>(r1, p, kbase, vbase, c1.blkA, c1.blkB, li, lq, c1.h);
+    load_tile<KT, D>(r1, kv, c1.blkA, c1.blkB, li, lq, c1.h);
     const bool has2 = has1 && tau + 2 < tau_end;
     Coord c2 = c1;
     if (has2) c2 = advance(p, ix, c1);

@@ -1,0 +1,177 @@
+// MFMA tile helpers shared by the paged decode and chunked-prefill kernels
+// (gfx950, v_mfma_f32_16x16x32_{bf16,f16}).
+//
+// A tile is 32 tokens (two 16-token blocks) of one KV head in the native
+// layout (K tile [bs][D], V tile [D][bs]).  Lane l (i = l % 16, q = l / 16)
+// of a wave loads:
+//   K rows of tokens 8*(i/4)%16 + i%4 and that + 4 (A operands of the two
+//   S^T = K Q^T chains), channels [q*D/4, (q+1)*D/4);
+//   V channel 16t + i, tokens 8q..8q+7 (B operand of O^T = V^T P^T).
+// With that assignment the QK output of lane (i, q) holds the scores of
+// column i for tokens 8q..8q+7, which is exactly the P^T operand the P.V
+// product needs from the same lane: no cross-lane shuffles between the two.
+#pragma once
+
+#include <type_traits>
+
+#include "cf_device.hpp"
+
+namespace cf {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// KV data is read once per call: non-temporal (streaming) loads.
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+template <class T>
+__device__ __forceinline__ T stream_load(const void* ptr);
+template <>
+__device__ __forceinline__ uint4 stream_load<uint4>(const void* ptr) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4_t*)ptr));
+}
+template <>
+__device__ __forceinline__ uint2 stream_load<uint2>(const void* ptr) {
+  return __builtin_bit_cast(uint2, __builtin_nontemporal_load((const u32x2_t*)ptr));
+}
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
+
+// 8 e4m3 codes (two dwords, byte order = element order) -> 8 bf16.
+__device__ __forceinline__ bf16x8_t e4m3x8_to_bf16(uint32_t lo, uint32_t hi) {
+  uint4 r;
+  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
+  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
+  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
+  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
+  return as_bf16x8(r);
+}
+
+template <int KT>
+struct KvTraits;
+template <>
+struct KvTraits<kE4M3> {
+  static constexpr int kBytes = 1;
+};
+template <>
+struct KvTraits<kBF16> {
+  static constexpr int kBytes = 2;
+};
+
+// Raw per-lane registers of one 32-token tile.
+template <int KT, int D>
+struct TileRegs {
+  static constexpr int KB = KvTraits<KT>::kBytes;
+  static constexpr int KCHUNK = D / 4 * KB / 16;  // uint4 per K row slice
+  static constexpr int NV = D / 16;
+  uint4 k1[KCHUNK];  // K row slice of token 8*(i/4) + i%4
+  uint4 k2[KCHUNK];  // ... and of that token + 4
+  // V: 8 tokens of one channel per PV MFMA (8 bytes e4m3, 16 bytes bf16)
+  using VT = typename std::conditional<KB == 1, uint2, uint4>::type;
+  VT v[NV];
+};
+
+// Loads one 32-token tile (blocks blkA, blkB of KV head h) in the native
+// layout: K tile [bs][D] (token rows), V tile [D][bs] (channel rows), each
+// (block, head) tile contiguous.  Inner offsets are compile-time constants
+// (immediate offsets of the loads); block/head strides are uniform.
+// Invalid blocks (id -1) read block 0 instead; their tokens are masked.
+// A paged KV cache in the native layout: base pointers and the block and
+// head strides (elements) of the K and V views.
+struct KvCacheView {
+  const uint8_t* k;
+  const uint8_t* v;
+  int64_t k_blk, k_head, v_blk, v_head;
+};
+
+template <int KT, int D>
+__device__ __forceinline__ void load_tile(TileRegs<KT, D>& r, const KvCacheView& kv, int blkA, int blkB, int li,
+                                          int lq, int h) {
+  constexpr int KB = KvTraits<KT>::kBytes;
+  using R = TileRegs<KT, D>;
+  const int64_t a = blkA < 0 ? 0 : blkA, bb = blkB < 0 ? 0 : blkB;
+  const uint8_t* kA = kv.k + (a * kv.k_blk + (int64_t)h * kv.k_head) * KB;
+  const uint8_t* kB = kv.k + (bb * kv.k_blk + (int64_t)h * kv.k_head) * KB;
+  const uint8_t* vA = kv.v + (a * kv.v_blk + (int64_t)h * kv.v_head) * KB;
+  const uint8_t* vB = kv.v + (bb * kv.v_blk + (int64_t)h * kv.v_head) * KB;
+  // K: lane (li, lq) reads token koff = 8*(li/4)%16 + li%4 (+4) of block A
+  // (li < 8) or B, channels [lq*D/4, (lq+1)*D/4).
+  const int koff = (8 * (li >> 2) + (li & 3)) & 15;
+  const uint8_t* k1 = (li < 8 ? kA : kB) + (koff * D + lq * (D / 4)) * KB;
+#pragma unroll
+  for (int c = 0; c < R::KCHUNK; ++c) {
+    r.k1[c] = stream_load<uint4>(k1 + 16 * c);
+    r.k2[c] = stream_load<uint4>(k1 + 4 * D * KB + 16 * c);
+  }
+  // V: lane (li, lq) reads channel 16t + li, tokens 8*(lq%2)..+7 of block A
+  // (lq < 2) or B.
+  const uint8_t* vp = (lq < 2 ? vA : vB) + (li * 16 + (lq & 1) * 8) * KB;
+#pragma unroll
+  for (int t = 0; t < R::NV; ++t) r.v[t] = stream_load<typename R::VT>(vp + t * 256 * KB);
+}
+
+// Keeps the first `nbytes` bytes of an 8-byte register pair, zeroing the rest.
+__device__ __forceinline__ uint2 keep_bytes(uint2 v, int nbytes) {
+  const uint64_t x = ((uint64_t)v.y << 32) | v.x;
+  const uint64_t m = nbytes >= 8 ? ~0ull : (nbytes <= 0 ? 0ull : ((1ull << (8 * nbytes)) - 1));
+  const uint64_t y = x & m;
+  return make_uint2((uint32_t)y, (uint32_t)(y >> 32));
+}
+
+// Zeroes the V elements of this lane's tokens >= n_valid (of its 8): cache
+// slots past a sequence's end may hold any bit pattern, NaN codes included,
+// and 0 * NaN would poison the sum.
+__device__ __forceinline__ uint2 mask_tokens(uint2 v, int n_valid) { return keep_bytes(v, n_valid); }
+__device__ __forceinline__ uint4 mask_tokens(uint4 v, int n_valid) {
+  const uint2 lo = keep_bytes(make_uint2(v.x, v.y), n_valid * 2);
+  const uint2 hi = keep_bytes(make_uint2(v.z, v.w), n_valid * 2 - 8);
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+template <int KT>
+__device__ __forceinline__ bf16x8_t k_operand(const uint4* raw, int c) {
+  if constexpr (KT == kE4M3) {
+    const uint4 u = raw[c >> 1];
+    return (c & 1) ? e4m3x8_to_bf16(u.z, u.w) : e4m3x8_to_bf16(u.x, u.y);
+  } else {
+    return as_bf16x8(raw[c]);
+  }
+}
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// 8 e4m3 codes -> 8 fp16 (exact: e4m3 values lie inside fp16's range and
+// precision).
+__device__ __forceinline__ f16x8_t e4m3x8_to_f16(uint32_t lo, uint32_t hi) {
+  uint4 r;
+  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false));
+  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true));
+  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false));
+  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true));
+  return __builtin_bit_cast(f16x8_t, r);
+}
+
+
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+}  // namespace
+}  // namespace cf

@@ -10,7 +10,10 @@ Added, backward-compatible:
     total), required when the caches hold float8_e4m3fn codes;
   - keyword-only `partition_tokens` (split-KV partition length);
   - `paged_attention_tensors`, the tensor-native entry the dict API wraps
-    (int32 block tables [B, Mb], int32 lengths [B], output [B, Hq, D]).
+    (int32 block tables [B, Mb], int32 lengths [B], output [B, Hq, D]);
+  - `chunked_prefill_attention`, the attention of a chunked-prefill step
+    (reference runtime/src/engine/scheduler.rs:178-226): query chunks
+    attending causally to their sequence's cached tokens and to themselves.
 """
 
 from __future__ import annotations
@@ -147,4 +150,51 @@ def paged_attention(
     return {rid: out[i] for i, rid in enumerate(rids)}
 
 
-__all__ = ["DEFAULT_PARTITION_TOKENS", "paged_attention", "paged_attention_tensors"]
+def chunked_prefill_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    q_start: torch.Tensor,
+    block_size: int = 16,
+    scale: float | None = None,
+    *,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Attention of prefill chunks over the paged cache.
+
+    Args:
+        q: [Tq, Hq, D] bf16, the query rows of all chunks.
+        k_cache, v_cache: [num_blocks, 16, Hkv, D] bf16 or float8_e4m3fn in
+            the native layout (cf_hip.layout.alloc_kv_cache); the chunk's
+            own K/V must already be written.
+        block_tables: int32 [N, Mb], one row per chunk's sequence.
+        seq_lens: int32 [N], tokens of each sequence including its chunk.
+        q_start: int32 [N + 1]; chunk n owns q rows [q_start[n], q_start[n+1]).
+        scale: softmax scale, default 1/sqrt(D).
+
+    Row i of a chunk of L rows is the token at position seq_lens[n] - L + i
+    and attends to positions [0, seq_lens[n] - L + i] (bottom-right causal;
+    with nothing cached this is causal self-attention of the chunk, as the
+    reference's flash_attention_fwd(is_causal=True),
+    kernels/flash_attention.py:179-202).
+
+    Returns:
+        [Tq, Hq, D] bf16.
+    """
+    _require_rocm(q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    block_tables, seq_lens, q_start = (t if t.dtype == torch.int32 else t.to(torch.int32)
+                                       for t in (block_tables, seq_lens, q_start))
+    return _ops.prefill_chunk(
+        q, k_cache, v_cache, block_tables, seq_lens, q_start, float(scale), int(block_size),
+        k_scale=k_scale, v_scale=v_scale, out=out, workspace=workspace,
+    )
+
+
+__all__ = ["DEFAULT_PARTITION_TOKENS", "chunked_prefill_attention", "paged_attention", "paged_attention_tensors"]

@@ -14,6 +14,10 @@ Ops:
                       (sf-dialect/include/Sf/HALOps.td:184-189).  kwargs:
                       seq_lens, block_size, scale, k_scale, v_scale,
                       partition_tokens.  Returns [B, Hq, D].
+  chunked_prefill_attention
+                      inputs [query, key_cache, value_cache, block_tables,
+                      seq_lens, q_start]; kwargs: block_size, scale,
+                      k_scale, v_scale.  Returns [Tq, Hq, D].
   kv_cache_write_fp8  inputs [k_new, v_new, slot_mapping, key_cache,
                       value_cache, k_scale, v_scale]; returns key_cache.
   fp8_amax_scale      inputs [x]; per-head scales [H] (head axis -2).
@@ -35,6 +39,7 @@ from python_runtime.hal.interface import OpExecutor
 # op name -> (min inputs, max inputs)
 _ARITY: dict[str, tuple[int, int]] = {
     "paged_attention": (4, 5),
+    "chunked_prefill_attention": (6, 6),
     "kv_cache_write_fp8": (7, 7),
     "fp8_amax_scale": (1, 1),
     "fp8_quantize": (2, 2),
@@ -55,6 +60,7 @@ class HipBackend(OpExecutor):
         self._partition_tokens = partition_tokens
         self._handlers: dict[str, Callable[..., torch.Tensor]] = {
             "paged_attention": self._paged_attention,
+            "chunked_prefill_attention": self._chunked_prefill,
             "kv_cache_write_fp8": self._kv_cache_write_fp8,
             "fp8_amax_scale": lambda inputs, **kw: _ops.fp8_amax_scale(inputs[0]),
             "fp8_quantize": lambda inputs, **kw: _ops.fp8_quantize(inputs[0], inputs[1]),
@@ -95,6 +101,15 @@ class HipBackend(OpExecutor):
             q, k_cache, v_cache, table, seq_lens, block_size, kw.get("scale"),
             k_scale=kw.get("k_scale"), v_scale=kw.get("v_scale"),
             partition_tokens=int(kw.get("partition_tokens", self._partition_tokens)),
+        )
+
+    def _chunked_prefill(self, inputs: list[Any], **kw: Any) -> torch.Tensor:
+        from kernels.paged_attention import chunked_prefill_attention
+
+        q, k_cache, v_cache, tables, seq_lens, q_start = inputs
+        return chunked_prefill_attention(
+            q, k_cache, v_cache, tables, seq_lens, q_start, int(kw.get("block_size", k_cache.shape[1])),
+            kw.get("scale"), k_scale=kw.get("k_scale"), v_scale=kw.get("v_scale"),
         )
 
     def _kv_cache_write_fp8(self, inputs: list[Any], **kw: Any) -> torch.Tensor:

@@ -1,0 +1,215 @@
+"""GPU parity of the chunked-prefill kernel (and the c5 mixed step).
+
+Small cases compare every row with the float64 oracle
+(oracle.paged_attention.paged_prefill_fp64).  The full c5 step checks
+size-independent properties: every prefill row equals the decode kernel
+run with the row's truncated length (the semantics' own reduction), the
+written FP8 codes equal the oracle encoder's bit for bit, and a sample of
+rows and decodes matches the float64 oracle.  Tolerances: bf16 outputs
+within max(2e-2, 1 bf16 ulp) of the exact value, cosine >= 0.9999.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from cf_hip import ops, workloads
+from kernels.paged_attention import chunked_prefill_attention, paged_attention_tensors
+from oracle import fp8 as ofp8
+from oracle.paged_attention import paged_attention_fp64, paged_prefill_fp64
+from tests.gpu_util import assert_close, codes
+
+pytestmark = pytest.mark.gpu
+
+
+def _write_new_rows(case, t):
+    """The step's cache write: e4m3 through the product kernel, bf16 by
+    plain indexing."""
+    if t["k_scale"] is not None:
+        ops.kv_write_fp8(t["k_new"], t["v_new"], t["slots"], t["k_cache"], t["v_cache"], t["k_scale"],
+                         t["v_scale"])
+    else:
+        bs = case.block_size
+        s = t["slots"]
+        t["k_cache"][s // bs, s % bs] = t["k_new"].to(t["k_cache"].dtype)
+        t["v_cache"][s // bs, s % bs] = t["v_new"].to(t["v_cache"].dtype)
+
+
+def _cache_values(kc, vc, used):
+    idx = torch.tensor(used, dtype=torch.long, device=kc.device)
+    kc, vc = kc[idx], vc[idx]
+    if kc.dtype == torch.float8_e4m3fn:
+        return ofp8.decode(codes(kc)), ofp8.decode(codes(vc))
+    return kc.float().cpu().numpy(), vc.float().cpu().numpy()
+
+
+def _remap(tables):
+    used = sorted({b for t in tables for b in t})
+    remap = {b: i for i, b in enumerate(used)}
+    return used, [[remap[b] for b in t] for t in tables]
+
+
+def oracle_prefill(case, t, q=None, tables=None, lens=None, q_start=None):
+    tables = [list(x) for x in (tables if tables is not None else case.prefill_tables)]
+    used, rt = _remap(tables)
+    k, v = _cache_values(t["k_cache"], t["v_cache"], used)
+    ks = t["k_scale"].cpu().numpy() if t["k_scale"] is not None else None
+    vs = t["v_scale"].cpu().numpy() if t["v_scale"] is not None else None
+    q = (q if q is not None else case.q_prefill).float().cpu().numpy()
+    return paged_prefill_fp64(q, k, v, rt, list(lens if lens is not None else case.prefill_lens),
+                              list(q_start if q_start is not None else case.q_start), case.block_size,
+                              case.scale, ks, vs)
+
+
+def _prefill(case, t, **kw):
+    out = chunked_prefill_attention(
+        kw.get("q", t["q_prefill"]), t["k_cache"], t["v_cache"], kw.get("tables", t["prefill_tables"]),
+        kw.get("lens", t["prefill_lens"]), kw.get("q_start", t["q_start"]), case.block_size, case.scale,
+        k_scale=t["k_scale"], v_scale=t["v_scale"], out=kw.get("out"),
+    )
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 1, 128), (32, 2, 64), (4, 2, 128),
+                                      (16, 8, 64)])
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_shapes_match_oracle(gpu, hq, hkv, d, kv_dtype):
+    print(f"[case] prefill hq={hq} hkv={hkv} d={d} kv={kv_dtype}", flush=True)
+    case = workloads.make_mixed_case(device=gpu, seed=hq + d, chunks=[1, 17, 64, 100, 33],
+                                     cached=[0, 5, 300, 33, 1000], decode_lens=[], num_q_heads=hq,
+                                     num_kv_heads=hkv, head_dim=d, kv_dtype=kv_dtype)
+    t = workloads.materialize_mixed(case)
+    _write_new_rows(case, t)
+    out = _prefill(case, t)
+    ref, covered = oracle_prefill(case, t)
+    assert covered.all()
+    assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, f"prefill {hq}/{hkv}/{d}/{kv_dtype}")
+
+
+@pytest.mark.parametrize("chunks,cached", [([512], [0]), ([512], [4096]), ([1] * 40, list(range(0, 4000, 100))),
+                                           ([700, 3], [17, 9000])])
+def test_chunk_mixes(gpu, chunks, cached):
+    print(f"[case] prefill chunks={chunks[:4]}.. cached={cached[:4]}..", flush=True)
+    case = workloads.make_mixed_case(device=gpu, seed=5, chunks=chunks, cached=cached, decode_lens=[])
+    t = workloads.materialize_mixed(case)
+    _write_new_rows(case, t)
+    out = _prefill(case, t)
+    ref, _ = oracle_prefill(case, t)
+    assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, "chunk mix")
+
+
+def test_edge_rules(gpu):
+    """Overlapping and empty chunks, rows outside every chunk (left as they
+    were), rows at negative positions (zeros), lengths past the table."""
+    case = workloads.make_mixed_case(device=gpu, seed=9, chunks=[40, 30, 20], cached=[10, 50, 0],
+                                     decode_lens=[])
+    t = workloads.materialize_mixed(case)
+    _write_new_rows(case, t)
+    q_start = [3, 45, 41, 41, 80]  # chunk 1 overlaps chunk 0; chunk 2 is empty after the cut
+    lens = [52, 20, 20, 5]  # chunk 3: 35 rows, 5 tokens -> 30 rows at negative positions
+    tables = case.prefill_tables + [case.prefill_tables[2]]
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=gpu)
+    qs_t = torch.tensor(q_start, dtype=torch.int32, device=gpu)
+    tab_t = workloads._int_tensor(tables, gpu)
+    sentinel = torch.full_like(t["q_prefill"], 7.0)
+    out = _prefill(case, t, tables=tab_t, lens=lens_t, q_start=qs_t, out=sentinel.clone())
+    ref, covered = oracle_prefill(case, t, tables=tables, lens=lens, q_start=q_start)
+    got = out.float().cpu().numpy()
+    assert (got[~covered] == 7.0).all()
+    assert covered.sum() == 77 and not covered[:3].any() and not covered[80:].any()
+    assert_close(got[covered], ref[covered], torch.bfloat16, "edge rules")
+    assert (got[45:75] == 0).all()
+    # a length past the table's capacity reads the table's tokens only
+    cap = len(case.prefill_tables[0]) * 16
+    lens2 = torch.tensor([cap + 100], dtype=torch.int32, device=gpu)
+    qs2 = torch.tensor([0, 8], dtype=torch.int32, device=gpu)
+    tab0 = workloads._int_tensor(case.prefill_tables[:1], gpu)  # exactly table 0's blocks
+    out2 = _prefill(case, t, q=t["q_prefill"][:8], tables=tab0, lens=lens2, q_start=qs2)
+    ref2, _ = oracle_prefill(case, t, q=case.q_prefill[:8], tables=case.prefill_tables[:1], lens=[cap + 100],
+                             q_start=[0, 8])
+    assert_close(out2.float().cpu().numpy(), ref2, torch.bfloat16, "past capacity")
+
+
+def test_repeated_calls_shrinking(gpu):
+    """Back-to-back calls through one cached workspace, the second smaller:
+    no state of the first leaks into the second."""
+    big = workloads.make_mixed_case(device=gpu, seed=12, chunks=[300, 200], cached=[2000, 100], decode_lens=[])
+    tb = workloads.materialize_mixed(big)
+    _write_new_rows(big, tb)
+    small = workloads.make_mixed_case(device=gpu, seed=13, chunks=[20], cached=[60], decode_lens=[])
+    ts = workloads.materialize_mixed(small)
+    _write_new_rows(small, ts)
+    for _ in range(2):
+        ob = _prefill(big, tb)
+        os_ = _prefill(small, ts)
+    assert_close(ob.float().cpu().numpy(), oracle_prefill(big, tb)[0], torch.bfloat16, "big")
+    assert_close(os_.float().cpu().numpy(), oracle_prefill(small, ts)[0], torch.bfloat16, "small")
+
+
+def test_c5_full_step(gpu):
+    """The full c5 step: write, decode, prefill on one stream."""
+    print("[case] c5 full step", flush=True)
+    case = workloads.make_mixed_case(device=gpu, seed=0)
+    t = workloads.materialize_mixed(case)
+    _write_new_rows(case, t)
+    dec = paged_attention_tensors(t["q_decode"], t["k_cache"], t["v_cache"], t["decode_tables"], t["decode_lens"],
+                                  16, case.scale, k_scale=t["k_scale"], v_scale=t["v_scale"])
+    pre = _prefill(case, t)
+
+    # written codes: bit-exact against the oracle encoder
+    kc_new = t["k_cache"].view(torch.uint8)[t["slots"] // 16, t["slots"] % 16]
+    vc_new = t["v_cache"].view(torch.uint8)[t["slots"] // 16, t["slots"] % 16]
+    ks, vs = t["k_scale"].cpu().numpy(), t["v_scale"].cpu().numpy()
+    want_k = ofp8.encode(case.k_new.float().cpu().numpy() / ks[None, :, None])
+    want_v = ofp8.encode(case.v_new.float().cpu().numpy() / vs[None, :, None])
+    assert np.array_equal(kc_new.cpu().numpy(), want_k)
+    assert np.array_equal(vc_new.cpu().numpy(), want_v)
+
+    # every prefill row == decode with the row's truncated length
+    rows_tables, rows_lens = [], []
+    for n, (c, ln) in enumerate(zip(case.meta["cached"], case.meta["chunks"])):
+        rows_tables += [case.prefill_tables[n]] * ln
+        rows_lens += [c + i + 1 for i in range(ln)]
+    rt = workloads._int_tensor(rows_tables, gpu)
+    rl = torch.tensor(rows_lens, dtype=torch.int32, device=gpu)
+    as_decode = paged_attention_tensors(t["q_prefill"], t["k_cache"], t["v_cache"], rt, rl, 16, case.scale,
+                                        k_scale=t["k_scale"], v_scale=t["v_scale"])
+    torch.cuda.synchronize()
+    assert_close(pre.float().cpu().numpy(), as_decode.float().cpu().numpy(), torch.bfloat16, "prefill vs decode")
+
+    # sampled rows and decodes against the float64 oracle
+    g = torch.Generator().manual_seed(1)
+    sample = sorted(set(torch.randint(0, len(rows_lens), (48,), generator=g).tolist()) | {0, 511, 4095})
+    used, remapped = _remap([rows_tables[i] for i in sample] + [case.decode_tables[i] for i in range(8)])
+    k, v = _cache_values(t["k_cache"], t["v_cache"], used)
+    qs = torch.cat([case.q_prefill[sample], case.q_decode[:8]]).float().cpu().numpy()
+    lens = [rows_lens[i] for i in sample] + case.decode_lens[:8]
+    ref = paged_attention_fp64(qs, k, v, remapped, lens, 16, case.scale, ks, vs)
+    got = torch.cat([pre[sample], dec[:8]]).float().cpu().numpy()
+    assert_close(got, ref, torch.bfloat16, "c5 sampled rows")
+
+
+def test_hal_op(gpu):
+    from python_runtime.hal.hip_backend import HipBackend
+
+    case = workloads.make_mixed_case(device=gpu, seed=14, chunks=[24, 9], cached=[40, 0], decode_lens=[])
+    t = workloads.materialize_mixed(case)
+    _write_new_rows(case, t)
+    out = HipBackend().execute(
+        "chunked_prefill_attention",
+        [t["q_prefill"], t["k_cache"], t["v_cache"], t["prefill_tables"], t["prefill_lens"], t["q_start"]],
+        scale=case.scale, k_scale=t["k_scale"], v_scale=t["v_scale"],
+    )
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), oracle_prefill(case, t)[0], torch.bfloat16, "hal")
+
+
+def test_rejects_unsupported(gpu):
+    case = workloads.make_mixed_case(device=gpu, seed=15, chunks=[4], cached=[0], decode_lens=[],
+                                     num_q_heads=6, num_kv_heads=2, head_dim=64)  # G = 3
+    t = workloads.materialize_mixed(case)
+    with pytest.raises(NotImplementedError):
+        _prefill(case, t)
