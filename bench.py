@@ -185,6 +185,8 @@ def main() -> None:
     ap.add_argument("--cpu-sample", type=int, default=8)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-shared-prefix", action="store_true",
+                    help="do not pass the shared-prefix statement (every sequence reads its whole table)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -208,8 +210,15 @@ def main() -> None:
         pools.append(workloads.materialize(case, args.layout))
     tables = case.tables_tensor(dev)
     lens = case.seq_lens_tensor(dev)
+    # The radix cache's statement of shared prefix blocks (what a serving
+    # loop passes along with the tables): the LCP of neighbouring tables.
+    shared = None
+    if not args.no_shared_prefix:
+        shared = torch.tensor(ops.shared_prefix_lens(case.block_tables, case.seq_lens, case.block_size),
+                              dtype=torch.int32, device=dev)
     plans = [
-        ops.DecodePlan(case.q, kc, vc, tables, lens, case.scale, case.block_size, ks, vs, args.partition)
+        ops.DecodePlan(case.q, kc, vc, tables, lens, case.scale, case.block_size, ks, vs, args.partition,
+                       shared_prefix_lens=shared)
         for kc, vc, ks, vs in pools
     ]
     ab = workloads.algorithmic_bytes(case)
@@ -278,6 +287,7 @@ def main() -> None:
             "partition_tokens": args.partition,
             "kv_layout": args.layout,
             "cache_pools_rotated": args.pools,
+            "shared_prefix_statement": shared is not None,
             "parallelism": "single GPU",
         },
         "hbm_gbs_step": ab["unique"] / (ms_step / 1e3) / 1e9,

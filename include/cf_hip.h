@@ -120,6 +120,34 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache,
                         CfTensor* out, void* workspace,
                         uint64_t workspace_bytes, void* stream);
 
+/* cf_paged_decode with a statement of which sequences share cached
+ * prefix blocks (the radix cache's shared prefixes, reference
+ * runtime/src/cache/radix.rs:50-177 and block.rs share_prefix:273-306).
+ *
+ *   shared_prefix_lens  [B] i32, or NULL (then this is cf_paged_decode):
+ *       the first shared_prefix_lens[b] tokens of sequence b are stored in
+ *       the same physical blocks, in the same table positions, as those of
+ *       sequence b - 1 (entry 0 is ignored; values are clipped to both
+ *       sequences' lengths; 0 = nothing shared).
+ *
+ * Results are those of cf_paged_decode on the same tables (up to the
+ * rounding of a different summation order).  The MFMA path reads a shared
+ * run of whole 32-token tiles once for up to 16/G consecutive sharing
+ * sequences instead of once per sequence; other paths ignore the hint.
+ * The statement is trusted: a claimed share the tables do not have makes
+ * the sharers read the first sharer's blocks (block ids stay range-checked,
+ * so no access leaves the cache).  Batches above 2048 sequences ignore it. */
+int32_t cf_paged_decode_shared(const CfTensor* q, const CfTensor* k_cache,
+                               const CfTensor* v_cache,
+                               const CfTensor* block_tables,
+                               const CfTensor* seq_lens,
+                               const CfTensor* shared_prefix_lens,
+                               const CfTensor* k_scale, const CfTensor* v_scale,
+                               float scale, int32_t block_size,
+                               int32_t partition_tokens, CfTensor* out,
+                               void* workspace, uint64_t workspace_bytes,
+                               void* stream);
+
 /* Workspace needed by cf_prefill_chunk_fp8 (on the current device) for
  * num_q_tokens query rows in num_chunks chunks.  Grows with the query
  * rows (one small record per query block), not with the cached context. */

@@ -64,6 +64,28 @@ def _cached_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return ws
 
 
+def shared_prefix_lens(block_tables: list[list[int]], seq_lens: list[int], block_size: int) -> list[int]:
+    """Tokens each sequence shares with the previous one (host-side).
+
+    Entry b is the number of leading tokens of sequence b stored in the
+    same physical blocks, at the same table positions, as those of
+    sequence b - 1: the longest common prefix of the two block tables, in
+    tokens, cut to both sequences' lengths (entry 0 is 0).  Consecutive
+    sequences that a radix-tree prefix cache placed on shared blocks
+    (reference runtime/src/cache/radix.rs:50-177, block.rs:273-306) get
+    their shared length; this is the `shared_prefix_lens` statement
+    `paged_decode` takes.
+    """
+    out = [0] * len(block_tables)
+    for b in range(1, len(block_tables)):
+        prev, cur = block_tables[b - 1], block_tables[b]
+        n, lim = 0, min(len(prev), len(cur))
+        while n < lim and int(prev[n]) == int(cur[n]):
+            n += 1
+        out[b] = max(0, min(n * block_size, int(seq_lens[b - 1]), int(seq_lens[b])))
+    return out
+
+
 def paged_decode(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -77,11 +99,17 @@ def paged_decode(
     partition_tokens: int = DEFAULT_PARTITION_TOKENS,
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    shared_prefix_lens: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Paged decode attention on the GPU; returns out [B, Hq, D] (dtype of q).
 
     workspace: optional buffer of decode_workspace_bytes() bytes; by default
     a cached one per (device, stream) is used.
+
+    shared_prefix_lens: optional int32 [B] device tensor, entry b = leading
+    tokens sequence b shares (same physical blocks) with sequence b - 1
+    (see `shared_prefix_lens()`); shared tiles are then read once per
+    group of sharing sequences.  The statement is trusted.
 
     block_tables: int32 [B, Mb]; seq_lens: int32 [B]; caches [NB, bs, Hkv, D]
     with any strides (f32/f16/bf16/e4m3fn); e4m3fn caches need per-KV-head
@@ -105,15 +133,20 @@ def paged_decode(
         ws_ptr = workspace.data_ptr()
     ks = descriptor(k_scale) if k_scale is not None else None
     vs = descriptor(v_scale) if v_scale is not None else None
+    dsh = None
+    if shared_prefix_lens is not None:
+        _require_device("shared_prefix_lens", shared_prefix_lens)
+        _same_device(q, shared_prefix_lens)
+        dsh = descriptor(shared_prefix_lens)
     dq, dk, dv = descriptor(q), descriptor(k_cache), descriptor(v_cache)
     dt, dsl, do = descriptor(block_tables), descriptor(seq_lens), descriptor(out)
     with torch.cuda.device(dev):
-        rc = lib().cf_paged_decode(
-            ref(dq), ref(dk), ref(dv), ref(dt), ref(dsl), ref(ks), ref(vs),
+        rc = lib().cf_paged_decode_shared(
+            ref(dq), ref(dk), ref(dv), ref(dt), ref(dsl), ref(dsh), ref(ks), ref(vs),
             float(scale), int(block_size), int(partition_tokens), ref(do),
             ws_ptr, need, stream_handle(dev),
         )
-    check(rc, "cf_paged_decode")
+    check(rc, "cf_paged_decode_shared")
     return out
 
 
@@ -196,32 +229,37 @@ class DecodePlan:
         v_scale: torch.Tensor | None = None,
         partition_tokens: int = DEFAULT_PARTITION_TOKENS,
         out: torch.Tensor | None = None,
+        shared_prefix_lens: torch.Tensor | None = None,
     ) -> None:
         for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("block_tables", block_tables),
                         ("seq_lens", seq_lens)):
             _require_device(name, t)
         self.device = _same_device(q, k_cache, v_cache, block_tables, seq_lens)
+        if shared_prefix_lens is not None:
+            _require_device("shared_prefix_lens", shared_prefix_lens)
+            _same_device(q, shared_prefix_lens)
         self.out = out if out is not None else torch.empty(q.shape, dtype=q.dtype, device=self.device)
         self.ws_bytes = decode_workspace_bytes(
             q.shape[0], q.shape[1], k_cache.shape[2], q.shape[2], block_tables.shape[1], block_size,
             partition_tokens,
         )
         self.workspace = new_workspace(self.ws_bytes, self.device)
-        self._keep = (q, k_cache, v_cache, block_tables, seq_lens, k_scale, v_scale)
+        self._keep = (q, k_cache, v_cache, block_tables, seq_lens, k_scale, v_scale, shared_prefix_lens)
         self._d = [descriptor(t) for t in (q, k_cache, v_cache, block_tables, seq_lens)]
+        self._dsh = descriptor(shared_prefix_lens) if shared_prefix_lens is not None else None
         self._ks = descriptor(k_scale) if k_scale is not None else None
         self._vs = descriptor(v_scale) if v_scale is not None else None
         self._do = descriptor(self.out)
         self._args = (
-            *(ref(d) for d in self._d), ref(self._ks), ref(self._vs), float(scale), int(block_size),
-            int(partition_tokens), ref(self._do), self.workspace.data_ptr() if self.ws_bytes else None,
-            self.ws_bytes,
+            *(ref(d) for d in self._d), ref(self._dsh), ref(self._ks), ref(self._vs), float(scale),
+            int(block_size), int(partition_tokens), ref(self._do),
+            self.workspace.data_ptr() if self.ws_bytes else None, self.ws_bytes,
         )
-        self._fn = lib().cf_paged_decode
+        self._fn = lib().cf_paged_decode_shared
 
     def run(self, stream: int | None = None) -> torch.Tensor:
         rc = self._fn(*self._args, stream if stream is not None else stream_handle(self.device))
-        check(rc, "cf_paged_decode")
+        check(rc, "cf_paged_decode_shared")
         return self.out
 
 
@@ -337,5 +375,6 @@ __all__ = [
     "fp8_quantize",
     "kv_write_fp8",
     "paged_decode",
+    "shared_prefix_lens",
     "_abi",
 ]

@@ -199,6 +199,16 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache, const CfTens
                         const CfTensor* block_tables, const CfTensor* seq_lens, const CfTensor* k_scale,
                         const CfTensor* v_scale, float scale, int32_t block_size, int32_t partition_tokens,
                         CfTensor* out, void* workspace, uint64_t workspace_bytes, void* stream) {
+  return cf_paged_decode_shared(q, k_cache, v_cache, block_tables, seq_lens, nullptr, k_scale, v_scale, scale,
+                                block_size, partition_tokens, out, workspace, workspace_bytes, stream);
+}
+
+int32_t cf_paged_decode_shared(const CfTensor* q, const CfTensor* k_cache, const CfTensor* v_cache,
+                               const CfTensor* block_tables, const CfTensor* seq_lens,
+                               const CfTensor* shared_prefix_lens, const CfTensor* k_scale,
+                               const CfTensor* v_scale, float scale, int32_t block_size,
+                               int32_t partition_tokens, CfTensor* out, void* workspace,
+                               uint64_t workspace_bytes, void* stream) {
   View vq, vk, vv, vt, vs, vo;
   int32_t rc;
   if ((rc = view_of(q, "q", 3, &vq))) return rc;
@@ -257,6 +267,15 @@ int32_t cf_paged_decode(const CfTensor* q, const CfTensor* k_cache, const CfTens
   p.t_sm = vt.stride[1];
   p.seq_lens = (const int32_t*)vs.base;
   p.sl_s = vs.stride[0];
+  if (shared_prefix_lens != nullptr) {
+    View vsh;
+    if ((rc = view_of(shared_prefix_lens, "shared_prefix_lens", 1, &vsh))) return rc;
+    CF_CHECK(vsh.dtype == CF_I32, "shared_prefix_lens: expected i32, got %s", dtype_name(vsh.dtype));
+    CF_CHECK(vsh.size[0] == B, "shared_prefix_lens has %lld entries, batch is %lld", (long long)vsh.size[0],
+             (long long)B);
+    p.shared = (const int32_t*)vsh.base;
+    p.sh_s = vsh.stride[0];
+  }
   p.out = vo.base;
   p.o_sb = vo.stride[0];
   p.o_sh = vo.stride[1];

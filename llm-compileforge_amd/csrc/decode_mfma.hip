@@ -4,32 +4,34 @@
 // :21-73): softmax(q.k * scale) . v over a sequence's first
 // min(seq_len, Mb*bs) tokens, query head h reading KV head h / G.
 //
-// Shape of the work
-//   One workgroup of NW waves per (partition, KV head, sequence).  A
-//   partition is PT tokens (a multiple of 32); each wave takes 32-token
-//   tiles (two 16-token blocks) round-robin.  The G query heads that share
-//   the KV head are the 16 columns of the MFMA tiles (zero-padded when
-//   G < 16), so every K/V byte is read once per workgroup.
-//
 // Per 32-token tile (v_mfma_f32_16x16x32_bf16, lane l: i = l % 16,
 // q = l / 16; an A operand row and a B operand column are indexed by i,
 // output rows by 4q + v):
 //   S^T = K Q^T   two MFMA chains (rows = tokens), D/32 MFMAs each.  Lane
 //                 (i, q) feeds the K row of token 8*(i/4) + i%4 (+4 for the
 //                 second chain), channels [q*D/4, (q+1)*D/4); the chains'
-//                 outputs land so that lane (i, q) holds the scores of head
-//                 i for the 8 consecutive tokens 8q..8q+7.
-//   online softmax per head (lane-local, plus a max across the 4 q groups).
+//                 outputs land so that lane (i, q) holds the scores of
+//                 column i for the 8 consecutive tokens 8q..8q+7.
+//   online softmax per column (lane-local, plus a max across the 4 q groups).
 //   O^T += V^T P^T  D/16 MFMAs; lane (i, q) feeds channel 16t + i of V for
 //                 tokens 8q..8q+7 -- 8 consecutive tokens of one channel,
 //                 which the native V layout ([NB, Hkv, D, bs]) stores
 //                 contiguously -- and its own 8 probabilities as P^T.  The
-//                 output holds O[head i][16t + 4q + v], so the softmax
+//                 output holds O[column i][16t + 4q + v], so the softmax
 //                 rescale stays lane-local.
-// e4m3 codes convert to bf16 exactly (v_cvt_scalef32_pk_bf16_fp8 with scale
-// 1.0); the per-KV-head dequant scales factor out of both products.
-// Workgroups combine their waves through LDS and write either the final
-// output (one partition) or (m, l, o) partials for decode_reduce.
+// The 16 MFMA columns are query heads: the G query heads of the tile's KV
+// head (zero-padded when G < 16), so each K/V byte is read once for all of
+// them.  e4m3 codes convert to bf16 exactly (v_cvt_scalef32_pk_bf16_fp8,
+// scale 1.0); the per-KV-head dequant scales factor out of both products.
+//
+// Shared prefixes (radix-cache blocks).  When the caller states, per
+// sequence, how many leading tokens it shares with the previous sequence
+// (same physical blocks), consecutive sequences that share at least
+// kMinShareTiles whole tiles form groups of up to 16/G members.  The
+// group's common tiles are read once, in a "prefix run" whose 16 columns
+// are the members' query heads (member m, head g -> column m*G + g); each
+// member then reads only its own remaining tiles.  A member's output is the
+// merge of its prefix partial and its own-run partial.
 #include "cf_device.hpp"
 #include "cf_host.hpp"
 #include "decode_params.hpp"
@@ -42,22 +44,34 @@ namespace {
 // ---------------------------------------------------------------------------
 // Work split: the "tile stream".
 //
-// Tiles are 32-token pieces of one sequence for one KV head, ordered
-// (KV head, sequence, tile).  With Tb = sum_b ceil(len_b / 32) tiles per head
-// and T = Hkv * Tb in all, wave w of the Wtot launched waves takes the
+// Within a KV head, runs are laid out sequence by sequence: a group
+// leader's prefix run (its group's shared tiles), then each sequence's own
+// run (its tiles after the shared prefix, all of them outside a group).
+// The stream is (KV head, run, tile); with Tb tiles per head and
+// T = Hkv * Tb in all, wave w of the Wtot launched waves takes the
 // contiguous range [w * chunk, min((w + 1) * chunk, T)), chunk = ceil(T /
 // Wtot): every wave gets the same number of tiles whatever the length mix,
 // and no workgroup is launched for nothing.  Inside its range a wave keeps
-// one online-softmax state per (sequence, KV head) run; a run that covers a
-// whole sequence is normalized and written to the output, a run that
-// covers part of one (it starts or ends at the wave's range boundary) is
-// written as an (m, l, o) partial into the wave's slot 0 (first run) or 1
-// (last run); decode_merge_kernel then combines the partials of every split
-// (sequence, KV head).  (Merging inside this kernel, by the last wave to
-// finish a split sequence, needs an agent-scope release per partial; on
+// one online-softmax state per run.  A run the wave holds whole is written
+// out: normalized to the output (a sequence outside any group), or as an
+// (m, l, o) record (a group member's own run, a prefix run).  A run split
+// between waves leaves an (m, l, o) partial in each wave's slot 0 (its
+// first run) or 1 (its last run).  decode_merge_kernel combines what each
+// (sequence, KV head) left.  (Merging inside this kernel, by the last wave
+// to finish a split sequence, needs an agent-scope release per partial; on
 // gfx950 that is an L2 writeback per flush and cost more than the separate
 // launch.)
+//
+// Partial rows (ws_o [rows][D] f32, ws_ml [rows][2]): wave slot s holds
+// rows [16 s, 16 s + 16), one per MFMA column; own-run records start at row
+// rec_own, G rows per (sequence, KV head); prefix records at rec_pre, G rows
+// per (member sequence, KV head).
 // ---------------------------------------------------------------------------
+
+constexpr int kPlanMaxB = 2048;    // batches up to this size keep a per-sequence plan in LDS
+constexpr int kMinShareTiles = 2;  // shortest shared prefix (32-token tiles) given a group run
+constexpr int kSlotCols = 16;      // columns of one partial slot (the MFMA width)
+constexpr int kOwn = 0, kPrefix = 1;
 
 // Read-only inputs the tile walk indexes with wave-uniform addresses.  Passed
 // as separate __restrict__ kernel arguments so the compiler may read them
@@ -80,10 +94,103 @@ __device__ __forceinline__ int ntiles_of(const DecodeParams& p, const Index& ix,
   return (eff_len(p, ix, b) + 31) >> 5;
 }
 
+// ---- per-sequence plan (LDS), built by wave 0 of every workgroup ----------
+struct Plan {
+  int len[kPlanMaxB];       // effective length
+  int j0[kPlanMaxB];        // first tile of the sequence's own run
+  int pre[kPlanMaxB];       // group leaders: prefix tiles | members << 24; others 0
+  int psum[kPlanMaxB + 1];  // first stream tile (within a KV head) of the sequence's runs
+};
 
+// Pass 1: lengths; j0 <- tiles shared with the previous sequence;
+// psum <- first member of the sequence's group.  A sequence sharing fewer
+// than kMinShareTiles tiles with its predecessor starts a group; groups are
+// cut every 16/G members.
+__device__ void plan_pass1(const DecodeParams& p, const Index& ix, const int32_t* shared, Plan* pl, int lane) {
+  const int SG = kSlotCols / p.G;
+  int carry_full = 0, carry_hs = 0;
+  for (int base = 0; base < p.B; base += 64) {
+    const int b = base + lane;
+    const int len = b < p.B ? eff_len(p, ix, b) : 0;
+    const int full = len >> 5;
+    int fprev = __shfl_up(full, 1, 64);
+    if (lane == 0) fprev = carry_full;
+    int lcpt = 0;
+    if (shared != nullptr && SG > 1 && b > 0 && b < p.B) {
+      const int sh = shared[(int64_t)b * p.sh_s];
+      lcpt = min(max(sh, 0) >> 5, min(full, fprev));
+    }
+    const bool hard = lcpt < kMinShareTiles;  // always true for b = 0
+    const int hs = max(wave_incl_max(hard ? b : -1, lane), carry_hs);
+    if (b < p.B) {
+      pl->len[b] = len;
+      pl->j0[b] = lcpt;
+      pl->psum[b] = hs + SG * ((b - hs) / SG);
+    }
+    carry_full = __shfl(full, 63, 64);
+    carry_hs = __shfl(hs, 63, 64);
+  }
+}
 
+// Pass 2: each group leader records its members and the tiles all of them
+// share (the minimum over the chain of neighbour shares).
+__device__ void plan_pass2(const DecodeParams& p, Plan* pl, int lane) {
+  const int SG = kSlotCols / p.G;
+  for (int base = 0; base < p.B; base += 64) {
+    const int b = base + lane;
+    if (b < p.B) {
+      int pre = 0;
+      if (pl->psum[b] == b) {
+        int n = 1, P = 1 << 23;
+        for (int k = 1; k < SG && b + k < p.B && pl->psum[b + k] == b; ++k) {
+          ++n;
+          P = min(P, pl->j0[b + k]);
+        }
+        if (n > 1) pre = P | (n << 24);
+      }
+      pl->pre[b] = pre;
+    }
+  }
+}
 
-// Tiles per KV head (sum over sequences).
+// Pass 3: j0 <- the group's shared tiles; psum <- exclusive scan of the
+// tiles of each sequence's runs (prefix run for leaders + own run).
+__device__ void plan_pass3(const DecodeParams& p, Plan* pl, int lane) {
+  int carry = 0;
+  for (int base = 0; base < p.B; base += 64) {
+    const int b = base + lane;
+    int rt = 0, j0 = 0;
+    if (b < p.B) {
+      const int lead = pl->psum[b];
+      j0 = pl->pre[lead] & 0xFFFFFF;
+      rt = (lead == b ? j0 : 0) + ((pl->len[b] + 31) >> 5) - j0;
+    }
+    const int incl = wave_incl_scan(rt, lane) + carry;
+    if (b < p.B) {
+      pl->j0[b] = j0;
+      pl->psum[b] = incl - rt;
+    }
+    carry = __shfl(incl, 63, 64);
+  }
+  if (lane == 0) pl->psum[p.B] = carry;
+}
+
+// Largest b with psum[b] <= r (64-ary search; psum[0] = 0 <= r).
+__device__ int plan_find(const Plan* pl, int B, int r, int lane) {
+  int lo = 0, n = B;
+  while (n > 1) {
+    const int step = (n + 63) >> 6;
+    const int off = lane * step;
+    const bool ok = off < n && pl->psum[lo + off] <= r;
+    const unsigned long long m = __ballot(ok);
+    const int idx = 63 - __clzll((long long)m);
+    lo = uniform(lo + idx * step);
+    n = uniform(min(step, n - idx * step));
+  }
+  return lo;
+}
+
+// ---- without a plan (batches above kPlanMaxB): no groups -------------------
 __device__ int tiles_per_head(const DecodeParams& p, const Index& ix, int lane) {
   int tb = 0;
   for (int base = 0; base < p.B; base += 64) {
@@ -113,11 +220,42 @@ __device__ void locate(const DecodeParams& p, const Index& ix, int r, int lane, 
   *before_out = running;
 }
 
+// Per-sequence lookups, from the LDS plan or (PL = false) from seq_lens.
+template <bool PL>
+struct Seqs {
+  const int32_t* __restrict__ lens;
+  int64_t sl_s;
+  int cap;  // table capacity in tokens
+  const Plan* pl;
+  __device__ __forceinline__ int len(int b) const {
+    if constexpr (PL) {
+      return uniform(pl->len[b]);
+    } else {
+      const int ctx = lens[(int64_t)b * sl_s];
+      return ctx < 0 ? 0 : (ctx < cap ? ctx : cap);
+    }
+  }
+  __device__ __forceinline__ int j0(int b) const {
+    if constexpr (PL) return uniform(pl->j0[b]);
+    else return 0;
+  }
+  __device__ __forceinline__ int pre(int b) const {
+    if constexpr (PL) return uniform(pl->pre[b]);
+    else return 0;
+  }
+  __device__ __forceinline__ int run_tiles(int b) const {
+    if constexpr (PL) return uniform(pl->psum[b + 1] - pl->psum[b]);
+    else return (len(b) + 31) >> 5;
+  }
+};
+
 struct Coord {
-  int h, b, j;  // KV head, sequence, tile within the sequence
-  int len;      // effective length of sequence b
-  int nt;       // tiles of sequence b
-  int blkA, blkB;  // physical blocks of the tile (-1: none / invalid)
+  int h, b, j;      // KV head, sequence (a prefix run: the group's leader), tile within the sequence
+  int kind;         // kOwn or kPrefix
+  int first, last;  // the run's tiles [first, last)
+  int len;          // effective length of sequence b
+  int ncols;        // MFMA columns in use: G, or members * G for a prefix run
+  int blkA, blkB;   // physical blocks of the tile (-1: none / invalid)
 };
 
 __device__ __forceinline__ int checked_block(const DecodeParams& p, const Index& ix, int b, int jb) {
@@ -131,53 +269,170 @@ __device__ __forceinline__ void fetch_ids(const DecodeParams& p, const Index& ix
   c.blkB = 2 * c.j + 1 < nblk ? checked_block(p, ix, c.b, 2 * c.j + 1) : -1;
 }
 
-// Next tile in stream order (the caller knows one exists).
-__device__ __forceinline__ Coord advance(const DecodeParams& p, const Index& ix, Coord c) {
-  if (c.j + 1 < c.nt) {
-    c.j += 1;
-  } else {
+__device__ __forceinline__ void own_run(Coord& c, int j0, int G) {
+  c.kind = kOwn;
+  c.first = j0;
+  c.last = (c.len + 31) >> 5;
+  c.ncols = G;
+  c.j = j0;
+}
+
+// First run of sequence b (the caller knows it has one).
+template <bool PL>
+__device__ __forceinline__ void enter_seq(const Seqs<PL>& s, Coord& c, int b, int G) {
+  c.b = b;
+  c.len = s.len(b);
+  const int pre = s.pre(b);
+  if (pre & 0xFFFFFF) {
+    c.kind = kPrefix;
+    c.first = 0;
+    c.last = pre & 0xFFFFFF;
+    c.ncols = (pre >> 24) * G;
     c.j = 0;
+  } else {
+    own_run(c, s.j0(b), G);
+  }
+}
+
+// Next tile in stream order (the caller knows one exists).
+template <bool PL>
+__device__ __forceinline__ Coord advance(const DecodeParams& p, const Index& ix, const Seqs<PL>& s, Coord c) {
+  if (c.j + 1 < c.last) {
+    c.j += 1;
+  } else if (c.kind == kPrefix && c.last < ((c.len + 31) >> 5)) {
+    own_run(c, c.last, p.G);  // the leader's own tiles follow its group's prefix
+  } else {
+    int b = c.b;
     do {
-      c.b += 1;
-      if (c.b == p.B) {
-        c.b = 0;
+      b += 1;
+      if (b == p.B) {
+        b = 0;
         c.h += 1;
       }
-      c.len = eff_len(p, ix, c.b);
-      c.nt = (c.len + 31) >> 5;
-    } while (c.nt == 0);
+    } while (s.run_tiles(b) == 0);
+    enter_seq(s, c, b, p.G);
   }
   fetch_ids(p, ix, c);
   return c;
 }
 
+// Q operand columns: column i < ncols is query head (i % G) of KV head h for
+// sequence b + i / G; the rest are zero.
 template <int D>
-__device__ __forceinline__ void load_q(bf16x8_t* qop, const DecodeParams& p, int b, int h, int li, int lq) {
+__device__ __forceinline__ void load_q(bf16x8_t* qop, const DecodeParams& p, const Coord& c, int li, int lq) {
   constexpr int NC = D / 32;
-  if (li < p.G) {
-    const uint16_t* qrow =
-        (const uint16_t*)p.q + (int64_t)b * p.q_sb + (int64_t)(h * p.G + li) * p.q_sh + lq * (D / 4);
+  if (li < c.ncols) {
+    const int m = li / p.G, g = li - m * p.G;
+    const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(c.b + m) * p.q_sb + (int64_t)(c.h * p.G + g) * p.q_sh +
+                           lq * (D / 4);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) qop[c] = as_bf16x8(*(const uint4*)(qrow + 8 * c));
+    for (int cc = 0; cc < NC; ++cc) qop[cc] = as_bf16x8(*(const uint4*)(qrow + 8 * cc));
   } else {
 #pragma unroll
-    for (int c = 0; c < NC; ++c) qop[c] = as_bf16x8(make_uint4(0, 0, 0, 0));
+    for (int cc = 0; cc < NC; ++cc) qop[cc] = as_bf16x8(make_uint4(0, 0, 0, 0));
   }
 }
 
-template <int KT, int D>
+// Writes out a finished run (normalized output, record or wave-slot
+// partial) and, from the wave holding the run's first tile, the merge
+// descriptors of the sequences it covers.
+template <bool PL, int D>
+__device__ __forceinline__ void flush_run(const DecodeParams& p, const Index& ix, const Plan* pl, const Coord& c,
+                                          const f32x4_t* o, float m, float l, int run_j0, bool first_run,
+                                          int64_t tau, int64_t chunk, int w, int lane) {
+  constexpr int NV = D / 16;
+  const int li = lane & 15, lq = lane >> 4;
+  const int G = p.G;
+  float lt = l + __shfl_xor(l, 16, 64);
+  lt += __shfl_xor(lt, 32, 64);
+  const float vs = ix.vscale ? ix.vscale[c.h * p.vs_s] : 1.0f;
+  const bool holds_first = run_j0 == c.first;
+  const bool complete = holds_first && c.j == c.last - 1;
+  const bool direct = complete && c.kind == kOwn && c.first == 0;  // a whole sequence outside any group
+  const int64_t bh = (int64_t)c.b * p.Hkv + c.h;
+  if (holds_first) {
+    int2 d = make_int2(0, 0);
+    if (!complete) {
+      // the run's stream tiles [s_tile, s_tile + len) span waves w1..w2; w1
+      // holds it in slot 1 unless the run starts its range
+      const int64_t s_tile = tau - (c.j - c.first);
+      const int64_t w1 = s_tile / chunk;
+      const int64_t w2 = (s_tile + (c.last - c.first) - 1) / chunk;
+      d = make_int2((int)((w1 * 2 + (w1 * chunk < s_tile ? 1 : 0)) * kSlotCols), (int)(w2 - w1 + 1));
+    }
+    if (c.kind == kOwn) {
+      if (lane == 0) {
+        if (complete && !direct) d = make_int2((int)(p.rec_own + bh * G), -1);
+        p.own_desc[bh] = d;
+        if (c.first == 0) p.pre_desc[bh] = make_int2(0, 0);
+      }
+    } else if (lane < c.ncols / G) {
+      const int64_t bm = (int64_t)(c.b + lane) * p.Hkv + c.h;
+      p.pre_desc[bm] = complete ? make_int2((int)(p.rec_pre + bm * G), -1) : make_int2(d.x + lane * G, d.y);
+      // a member whose tokens all lie in the shared prefix has no own run
+      if constexpr (PL) {
+        if (((pl->len[c.b + lane] + 31) >> 5) == c.last) p.own_desc[bm] = make_int2(0, 0);
+      }
+    }
+  }
+  if (li >= c.ncols) return;
+  if (direct) {
+    const float inv = lt > 0.0f ? vs / lt : 0.0f;
+    uint16_t* orow = (uint16_t*)p.out + (int64_t)c.b * p.o_sb + (int64_t)(c.h * G + li) * p.o_sh + 4 * lq;
+#pragma unroll
+    for (int t = 0; t < NV; ++t) {
+      uint2 packed;
+      packed.x = (uint32_t)bf16_bits_from_f32(o[t][0] * inv) | ((uint32_t)bf16_bits_from_f32(o[t][1] * inv) << 16);
+      packed.y = (uint32_t)bf16_bits_from_f32(o[t][2] * inv) | ((uint32_t)bf16_bits_from_f32(o[t][3] * inv) << 16);
+      *(uint2*)(orow + 16 * t) = packed;
+    }
+    return;
+  }
+  int64_t row;
+  if (!complete) {
+    row = ((int64_t)w * 2 + (first_run ? 0 : 1)) * kSlotCols + li;
+  } else if (c.kind == kOwn) {
+    row = p.rec_own + bh * G + li;
+  } else {
+    const int mm = li / G;
+    row = p.rec_pre + ((int64_t)(c.b + mm) * p.Hkv + c.h) * G + (li - mm * G);
+  }
+  float* os = p.ws_o + row * D + 4 * lq;
+#pragma unroll
+  for (int t = 0; t < NV; ++t)
+    *(float4*)(os + 16 * t) = make_float4(o[t][0] * vs, o[t][1] * vs, o[t][2] * vs, o[t][3] * vs);
+  if (lq == 0) {
+    p.ws_ml[row * 2] = m == -INFINITY ? -INFINITY : m * (1.0f / kLog2e);
+    p.ws_ml[row * 2 + 1] = lt;
+  }
+}
+
+template <int KT, int D, bool PL>
 __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, const int32_t* __restrict__ tables,
                                                             const int32_t* __restrict__ lens,
                                                             const float* __restrict__ kscale,
-                                                            const float* __restrict__ vscale) {
+                                                            const float* __restrict__ vscale,
+                                                            const int32_t* __restrict__ shared) {
+  extern __shared__ int dyn_lds[];
+  Plan* pl = reinterpret_cast<Plan*>(dyn_lds);
   const Index ix{tables, lens, kscale, vscale};
+  const Seqs<PL> seqs{lens, p.sl_s, p.Mb * 16, pl};
   constexpr int NC = D / 32;
   constexpr int NV = D / 16;
   const int lane = threadIdx.x & 63;
   const int li = lane & 15, lq = lane >> 4;
-  const int w = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int wave = uniform(threadIdx.x >> 6);
+  const int w = uniform(blockIdx.x * 4 + wave);
   const int Wtot = gridDim.x * 4;
-  const int G = p.G;
+
+  if constexpr (PL) {
+    if (wave == 0) plan_pass1(p, ix, shared, pl, lane);
+    __syncthreads();
+    if (wave == 0) plan_pass2(p, pl, lane);
+    __syncthreads();
+    if (wave == 0) plan_pass3(p, pl, lane);
+    __syncthreads();
+  }
 
   // Sequences with no tokens get zero rows (no tile of theirs is ever
   // visited); wave w takes sequences w, w + Wtot, ...
@@ -185,10 +440,15 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     if (eff_len(p, ix, bz) == 0) {
       uint16_t* orow = (uint16_t*)p.out + (int64_t)bz * p.o_sb;
       for (int e = lane; e < p.Hq * D; e += 64) orow[(int64_t)(e / D) * p.o_sh + e % D] = 0;
-      for (int hh = lane; hh < p.Hkv; hh += 64) p.merge_desc[(int64_t)bz * p.Hkv + hh] = make_int2(0, 0);
+      for (int hh = lane; hh < p.Hkv; hh += 64) {
+        p.own_desc[(int64_t)bz * p.Hkv + hh] = make_int2(0, 0);
+        p.pre_desc[(int64_t)bz * p.Hkv + hh] = make_int2(0, 0);
+      }
     }
   }
-  const int Tb = tiles_per_head(p, ix, lane);
+  int Tb;
+  if constexpr (PL) Tb = uniform(pl->psum[p.B]);
+  else Tb = tiles_per_head(p, ix, lane);
   const int64_t T = (int64_t)p.Hkv * Tb;
   if (T == 0) return;
   const int64_t chunk = (T + Wtot - 1) / Wtot;
@@ -199,24 +459,35 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   Coord c0;
   c0.h = uniform((int)(tau / Tb));
   {
-    int b, before;
-    locate(p, ix, (int)(tau % Tb), lane, &b, &before);
-    c0.b = b;
-    c0.j = uniform((int)(tau % Tb) - before);
+    const int r = uniform((int)(tau % Tb));
+    if constexpr (PL) {
+      const int b = plan_find(pl, p.B, r, lane);
+      const int o = r - uniform(pl->psum[b]);
+      enter_seq(seqs, c0, b, p.G);
+      if (c0.kind == kPrefix && o >= c0.last) {
+        own_run(c0, c0.last, p.G);
+        c0.j = c0.first + (o - (int)(seqs.pre(b) & 0xFFFFFF));
+      } else {
+        c0.j = c0.first + o;
+      }
+    } else {
+      int b, before;
+      locate(p, ix, r, lane, &b, &before);
+      enter_seq(seqs, c0, b, p.G);
+      c0.j = r - before;
+    }
   }
-  c0.len = eff_len(p, ix, c0.b);
-  c0.nt = (c0.len + 31) >> 5;
   fetch_ids(p, ix, c0);
   Coord c1 = c0;
   bool has1 = tau + 1 < tau_end;
-  if (has1) c1 = advance(p, ix, c0);
+  if (has1) c1 = advance(p, ix, seqs, c0);
 
   const KvCacheView kv{(const uint8_t*)p.k, (const uint8_t*)p.v, p.k_s[0], p.k_s[2], p.v_s[0], p.v_s[2]};
   TileRegs<KT, D> r0, r1;
   load_tile<KT, D>(r0, kv, c0.blkA, c0.blkB, li, lq, c0.h);
 
   bf16x8_t qop[NC];
-  load_q<D>(qop, p, c0.b, c0.h, li, lq);
+  load_q<D>(qop, p, c0, li, lq);
   float m = -INFINITY, l = 0.0f;
   f32x4_t o[NV];
 #pragma unroll
@@ -231,7 +502,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     load_tile<KT, D>(r1, kv, c1.blkA, c1.blkB, li, lq, c1.h);
     const bool has2 = has1 && tau + 2 < tau_end;
     Coord c2 = c1;
-    if (has2) c2 = advance(p, ix, c1);
+    if (has2) c2 = advance(p, ix, seqs, c1);
 
     // ---- S^T = K Q^T ---------------------------------------------------
     const float ks = ix.kscale ? ix.kscale[c0.h * p.ks_s] : 1.0f;
@@ -242,7 +513,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
       s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_operand<KT>(r0.k1, c), qop[c], s1, 0, 0, 0);
       s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_operand<KT>(r0.k2, c), qop[c], s2, 0, 0, 0);
     }
-    // lane (li, lq): s1[v] -> token 8lq + v, s2[v] -> token 8lq + 4 + v, head li
+    // lane (li, lq): s1[v] -> token 8lq + v, s2[v] -> token 8lq + 4 + v, column li
     float sc[8];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -315,48 +586,10 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
       }
     }
 
-    // ---- end of a (sequence, head) run ------------------------------------
-    const bool run_ends = !has1 || c1.b != c0.b || c1.h != c0.h;
+    // ---- end of a run -----------------------------------------------------
+    const bool run_ends = !has1 || c1.b != c0.b || c1.h != c0.h || c1.kind != c0.kind;
     if (run_ends) {
-      float lt = l + __shfl_xor(l, 16, 64);
-      lt += __shfl_xor(lt, 32, 64);
-      const float vs = ix.vscale ? ix.vscale[c0.h * p.vs_s] : 1.0f;
-      const bool complete = run_j0 == 0 && c0.j == c0.nt - 1;
-      if (run_j0 == 0 && lane == 0) {
-        // The wave holding a sequence's first tile tells the merge kernel
-        // what to do: nothing (complete here) or which slots to combine.
-        int2 desc = make_int2(0, 0);
-        if (!complete) {
-          const int64_t s_tile = tau - c0.j;
-          const int w1 = (int)(s_tile / chunk);
-          const int w2 = (int)((s_tile + c0.nt - 1) / chunk);
-          desc = make_int2(w1 * 2 + ((int64_t)w1 * chunk < s_tile ? 1 : 0), w2 - w1 + 1);
-        }
-        p.merge_desc[(int64_t)c0.b * p.Hkv + c0.h] = desc;
-      }
-      if (li < G) {
-        if (complete) {
-          const float inv = lt > 0.0f ? vs / lt : 0.0f;
-          uint16_t* orow = (uint16_t*)p.out + (int64_t)c0.b * p.o_sb + (int64_t)(c0.h * G + li) * p.o_sh + 4 * lq;
-#pragma unroll
-          for (int t = 0; t < NV; ++t) {
-            uint2 packed;
-            packed.x = (uint32_t)bf16_bits_from_f32(o[t][0] * inv) | ((uint32_t)bf16_bits_from_f32(o[t][1] * inv) << 16);
-            packed.y = (uint32_t)bf16_bits_from_f32(o[t][2] * inv) | ((uint32_t)bf16_bits_from_f32(o[t][3] * inv) << 16);
-            *(uint2*)(orow + 16 * t) = packed;
-          }
-        } else {
-          const int64_t slot = (int64_t)w * 2 + (first_run ? 0 : 1);
-          float* os = p.ws_o + (slot * G + li) * D + 4 * lq;
-#pragma unroll
-          for (int t = 0; t < NV; ++t)
-            *(float4*)(os + 16 * t) = make_float4(o[t][0] * vs, o[t][1] * vs, o[t][2] * vs, o[t][3] * vs);
-          if (lq == 0) {
-            p.ws_ml[(slot * G + li) * 2] = m == -INFINITY ? -INFINITY : m * (1.0f / kLog2e);
-            p.ws_ml[(slot * G + li) * 2 + 1] = lt;
-          }
-        }
-      }
+      flush_run<PL, D>(p, ix, pl, c0, o, m, l, run_j0, first_run, tau, chunk, w, lane);
       first_run = false;
     }
     if (!has1) break;
@@ -367,7 +600,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     r0 = r1;
     ++tau;
     if (run_ends) {
-      load_q<D>(qop, p, c0.b, c0.h, li, lq);
+      load_q<D>(qop, p, c0, li, lq);
       m = -INFINITY;
       l = 0.0f;
 #pragma unroll
@@ -377,25 +610,33 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   }
 }
 
-// Combines the (m, l, o) partials of each (sequence b, KV head h) whose
-// tiles were split between waves w1..w2 and writes the normalized rows;
-// sequences processed whole by one wave were written by the decode kernel.
-// One wave per (h, b).  Wave w1 holds the run in slot 2*w1 + 1 if the run
-// was not its first, else 2*w1; later waves in their slot 0.
+// Row of the k-th partial a merge descriptor names: {row, -1} is one
+// record; {row, n} is n wave-slot rows, the first at `row` (slot * 16 +
+// column), then slot 0 of each following wave at the same column.
+__device__ __forceinline__ int64_t part_row(int2 d, int k) {
+  if (d.y < 0 || k == 0) return d.x;
+  const int w1 = (d.x / kSlotCols) >> 1;
+  const int col = d.x % kSlotCols;
+  return (int64_t)(2 * (w1 + k)) * kSlotCols + col;
+}
+
+// Combines the (m, l, o) partials of each (sequence b, KV head h) that the
+// decode kernel did not write whole: its own run's and its group's prefix
+// run's, each a record or the wave slots of a split run.  One wave per
+// (h, b); partial rows hold the G heads of h in consecutive rows.
 template <int D, int G>
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p, const int32_t* __restrict__ lens, int Wtot) {
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
   constexpr int E = G * D / 64;  // output elements per lane
   __shared__ float wgt[64][G];
   __shared__ float inv_l[G];
   const int h = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x;
-  const int2 desc = p.merge_desc[(int64_t)b * p.Hkv + h];
-  const int nslots = desc.y;
-  if (nslots == 0) return;  // written whole by the decode kernel (or empty)
-  const int slot_first = desc.x;
-  const int w1 = slot_first >> 1;
-  (void)lens;
-  (void)Wtot;
+  const int2 dn = p.own_desc[(int64_t)b * p.Hkv + h];
+  const int2 dp = p.pre_desc[(int64_t)b * p.Hkv + h];
+  const int nown = dn.y < 0 ? 1 : dn.y;
+  const int npre = dp.y < 0 ? 1 : dp.y;
+  const int nsrc = nown + npre;
+  if (nsrc == 0) return;  // written whole by the decode kernel (or empty)
   float acc[E];
 #pragma unroll
   for (int i = 0; i < E; ++i) acc[i] = 0.0f;
@@ -405,19 +646,19 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p, const 
     Mg[g] = -INFINITY;
     Lg[g] = 0.0f;
   }
-  // Slots are taken 64 at a time; the running max per head rescales what
-  // earlier rounds accumulated (lane-local sums, merged at the end).
-  for (int k0 = 0; k0 < nslots; k0 += 64) {
-    const int kn = min(64, nslots - k0);
+  // Partials are taken 64 at a time; the running max per head rescales what
+  // earlier rounds accumulated.
+  for (int k0 = 0; k0 < nsrc; k0 += 64) {
+    const int kn = min(64, nsrc - k0);
     const int k = k0 + lane;
-    const int slot = k == 0 ? slot_first : 2 * (w1 + k);
+    const int64_t row = k < nown ? part_row(dn, k) : part_row(dp, k - nown);
     float m[G], l[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       m[g] = -INFINITY;
       l[g] = 0.0f;
       if (lane < kn) {
-        const float2 ml = *(const float2*)(p.ws_ml + ((int64_t)slot * G + g) * 2);
+        const float2 ml = *(const float2*)(p.ws_ml + (row + g) * 2);
         m[g] = ml.x;
         l[g] = ml.y;
       }
@@ -437,8 +678,9 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p, const 
 #pragma unroll
     for (int i = 0; i < E; ++i) acc[i] *= scale_old[(lane + 64 * i) / D];
     for (int kk = 0; kk < kn; ++kk) {
-      const int sk = (k0 + kk) == 0 ? slot_first : 2 * (w1 + k0 + kk);
-      const float* o = p.ws_o + (int64_t)sk * G * D;
+      const int ks = k0 + kk;
+      const int64_t rk = ks < nown ? part_row(dn, ks) : part_row(dp, ks - nown);
+      const float* o = p.ws_o + rk * D;
 #pragma unroll
       for (int i = 0; i < E; ++i) {
         const int idx = lane + 64 * i;
@@ -480,44 +722,47 @@ int cu_count() {
 // the randomly placed KV blocks faster on MI355X than two or three: more
 // concurrent streams of 2 KiB chunks cost more than the latency they hide
 // (measured: 115.6 us vs 121.1 us vs 125.4 us for 1/2/3 per CU on the
-// Llama-3-8B shape).  kMaxStreamBlocksPerCU bounds workspace sizes.
+// Llama-3-8B shape).  The workspace holds slots for this many waves.
 constexpr int kStreamBlocksPerCU = 1;
-constexpr int kMaxStreamBlocksPerCU = 4;
 
-template <int KT, int D>
+template <int KT, int D, bool PL>
 int blocks_per_cu() {
   static int cached = 0;
   if (cached == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<KT, D>, 256, 0) != hipSuccess || n < 1)
+    const size_t lds = PL ? sizeof(Plan) : 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<KT, D, PL>, 256, lds) != hipSuccess ||
+        n < 1)
       n = 1;
     cached = n < kStreamBlocksPerCU ? n : kStreamBlocksPerCU;
   }
   return cached;
 }
 
-template <int KT, int D>
-int32_t launch_stream_t(const DecodeParams& p0, hipStream_t stream) {
-  DecodeParams p = p0;
-  const int blocks = cu_count() * blocks_per_cu<KT, D>();
-  {
-    ProfileScope prof("cf_decode_mfma", stream);
-    hipLaunchKernelGGL((decode_stream_kernel<KT, D>), dim3(blocks), dim3(256), 0, stream, p, p.tables, p.seq_lens,
-                       p.k_scale, p.v_scale);
-  }
+template <int KT, int D, bool PL>
+int32_t launch_stream_t(const DecodeParams& p, hipStream_t stream) {
+  const int blocks = cu_count() * blocks_per_cu<KT, D, PL>();
+  ProfileScope prof("cf_decode_mfma", stream);
+  hipLaunchKernelGGL((decode_stream_kernel<KT, D, PL>), dim3(blocks), dim3(256), PL ? sizeof(Plan) : 0, stream, p,
+                     p.tables, p.seq_lens, p.k_scale, p.v_scale, PL ? p.shared : nullptr);
   CF_HIP_CHECK(hipGetLastError());
-  {
-    const dim3 grid(p.Hkv, p.B);
-    const int Wtot = blocks * 4;
-    ProfileScope prof("cf_decode_merge", stream);
-    switch (p.G) {
-      case 1: hipLaunchKernelGGL((decode_merge_kernel<D, 1>), grid, dim3(64), 0, stream, p, p.seq_lens, Wtot); break;
-      case 2: hipLaunchKernelGGL((decode_merge_kernel<D, 2>), grid, dim3(64), 0, stream, p, p.seq_lens, Wtot); break;
-      case 4: hipLaunchKernelGGL((decode_merge_kernel<D, 4>), grid, dim3(64), 0, stream, p, p.seq_lens, Wtot); break;
-      case 8: hipLaunchKernelGGL((decode_merge_kernel<D, 8>), grid, dim3(64), 0, stream, p, p.seq_lens, Wtot); break;
-      case 16: hipLaunchKernelGGL((decode_merge_kernel<D, 16>), grid, dim3(64), 0, stream, p, p.seq_lens, Wtot); break;
-      default: set_error("MFMA decode: unsupported GQA group %d", p.G); return CF_ERR_UNSUPPORTED;
-    }
+  return CF_OK;
+}
+
+template <int KT, int D>
+int32_t launch_t(const DecodeParams& p, hipStream_t stream) {
+  const int32_t rc = p.B <= kPlanMaxB ? launch_stream_t<KT, D, true>(p, stream)
+                                      : launch_stream_t<KT, D, false>(p, stream);
+  if (rc) return rc;
+  const dim3 grid(p.Hkv, p.B);
+  ProfileScope prof("cf_decode_merge", stream);
+  switch (p.G) {
+    case 1: hipLaunchKernelGGL((decode_merge_kernel<D, 1>), grid, dim3(64), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((decode_merge_kernel<D, 2>), grid, dim3(64), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((decode_merge_kernel<D, 4>), grid, dim3(64), 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((decode_merge_kernel<D, 8>), grid, dim3(64), 0, stream, p); break;
+    case 16: hipLaunchKernelGGL((decode_merge_kernel<D, 16>), grid, dim3(64), 0, stream, p); break;
+    default: set_error("MFMA decode: unsupported GQA group %d", p.G); return CF_ERR_UNSUPPORTED;
   }
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
@@ -525,27 +770,36 @@ int32_t launch_stream_t(const DecodeParams& p0, hipStream_t stream) {
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
-}  // namespace
-
-// Workspace layout: [o partials: 2 slots per wave x G x D f32, 256-byte
-// padded] [(m, l): 2 slots per wave x G x 2 f32, padded] [merge descriptors:
-// one int2 per (sequence, KV head)].
-namespace {
-uint64_t stream_waves() { return (uint64_t)cu_count() * kMaxStreamBlocksPerCU * 4; }
+// Workspace layout: [partial rows: o, D f32 each, 256-byte padded]
+// [(m, l) per row, padded] [own-run descriptors: int2 per (sequence, KV
+// head), padded] [prefix descriptors, same].  Rows: 2 slots x 16 columns per
+// wave, then G own-run and G prefix records per (sequence, KV head).
+uint64_t stream_waves() { return (uint64_t)cu_count() * kStreamBlocksPerCU * 4; }
 uint64_t pad256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
-uint64_t stream_o_bytes(int64_t G, int64_t D) { return pad256(stream_waves() * 2 * G * D * 4); }
-uint64_t stream_ml_bytes(int64_t G) { return pad256(stream_waves() * 2 * G * 2 * 4); }
+uint64_t slot_rows() { return stream_waves() * 2 * kSlotCols; }
+uint64_t total_rows(int64_t batch, int64_t num_q_heads) { return slot_rows() + 2 * (uint64_t)batch * num_q_heads; }
+
 }  // namespace
 
 uint64_t decode_mfma_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim) {
-  const int64_t G = num_kv_heads > 0 ? num_q_heads / num_kv_heads : num_q_heads;
-  return stream_o_bytes(G, head_dim) + stream_ml_bytes(G) + (uint64_t)batch * num_kv_heads * 8;
+  const uint64_t rows = total_rows(batch, num_q_heads);
+  const uint64_t desc = pad256((uint64_t)batch * num_kv_heads * 8);
+  return pad256(rows * head_dim * 4) + pad256(rows * 2 * 4) + 2 * desc;
 }
 
 void decode_mfma_bind_workspace(DecodeParams& p, void* workspace) {
-  p.ws_o = (float*)workspace;
-  p.ws_ml = (float*)((char*)workspace + stream_o_bytes(p.G, p.D));
-  p.merge_desc = (int2*)((char*)workspace + stream_o_bytes(p.G, p.D) + stream_ml_bytes(p.G));
+  const uint64_t rows = total_rows(p.B, p.Hq);
+  const uint64_t desc = pad256((uint64_t)p.B * p.Hkv * 8);
+  char* w = (char*)workspace;
+  p.ws_o = (float*)w;
+  w += pad256(rows * p.D * 4);
+  p.ws_ml = (float*)w;
+  w += pad256(rows * 2 * 4);
+  p.own_desc = (int2*)w;
+  w += desc;
+  p.pre_desc = (int2*)w;
+  p.rec_own = (int64_t)slot_rows();
+  p.rec_pre = p.rec_own + (int64_t)p.B * p.Hq;
 }
 
 bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
@@ -554,14 +808,14 @@ bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
   if (p.bs != 16 || (p.D != 64 && p.D != 128)) return false;
   if (p.G != 1 && p.G != 2 && p.G != 4 && p.G != 8 && p.G != 16) return false;
   if (p.NB < 1) return false;  // invalid block ids are redirected to block 0 (then masked)
+  // partial-row indices and descriptors are int32
+  if ((uint64_t)total_rows(p.B, p.Hq) >= (uint64_t)INT32_MAX / 2) return false;
   const int kb = kv_dt == kE4M3 ? 1 : 2;
   // Native layout: K tile [bs][D] (token stride D, channel stride 1), V tile
   // [D][bs] (token stride 1, channel stride bs); block/head strides free.
   if (p.k_s[3] != 1 || p.k_s[1] != p.D || p.v_s[1] != 1 || p.v_s[3] != 16) return false;
   for (int i = 0; i < 3; ++i)
     if ((p.k_s[i] * kb) % 16 != 0) return false;
-  // V: token stride 1 (channel-major blocks), runs of 8 tokens aligned.
-  if (p.v_s[1] != 1) return false;
   if ((p.v_s[0] * kb) % 16 != 0 || (p.v_s[2] * kb) % 16 != 0 || (p.v_s[3] * kb) % 16 != 0) return false;
   if (!aligned16(p.k) || !aligned16(p.v)) return false;
   // q rows: 16-byte aligned slices; out rows: 8-byte aligned groups of 4.
@@ -573,11 +827,11 @@ bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
 int32_t launch_decode_mfma(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream) {
   (void)q_dt;
   if (kv_dt == kE4M3) {
-    if (p.D == 128) return launch_stream_t<kE4M3, 128>(p, stream);
-    if (p.D == 64) return launch_stream_t<kE4M3, 64>(p, stream);
+    if (p.D == 128) return launch_t<kE4M3, 128>(p, stream);
+    if (p.D == 64) return launch_t<kE4M3, 64>(p, stream);
   } else {
-    if (p.D == 128) return launch_stream_t<kBF16, 128>(p, stream);
-    if (p.D == 64) return launch_stream_t<kBF16, 64>(p, stream);
+    if (p.D == 128) return launch_t<kBF16, 128>(p, stream);
+    if (p.D == 64) return launch_t<kBF16, 64>(p, stream);
   }
   set_error("MFMA decode: unsupported head_dim %d", p.D);
   return CF_ERR_UNSUPPORTED;

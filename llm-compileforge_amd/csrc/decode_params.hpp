@@ -18,14 +18,20 @@ struct DecodeParams {
   int64_t t_sb, t_sm;  // block_tables [B, Mb]
   const int32_t* seq_lens;
   int64_t sl_s;  // seq_lens [B]
+  const int32_t* shared;  // optional [B]: leading tokens sequence b shares with b - 1
+  int64_t sh_s;
   const float* k_scale;
   const float* v_scale;
   int64_t ks_s, vs_s;  // 0 when the scale is a single value
   void* out;
   int64_t o_sb, o_sh;  // out [B, Hq, D], D stride 1
-  float* ws_o;         // [B, Hq, max_parts, D] un-normalized partial outputs
-  float* ws_ml;        // [B, Hq, max_parts, 2] running max and sum
-  int2* merge_desc;    // MFMA path: per (sequence, KV head) {first slot, slot count}
+  float* ws_o;         // generic path: [B, Hq, max_parts, D] un-normalized partial outputs;
+                       // MFMA path: [rows, D] partial rows (see decode_mfma.hip)
+  float* ws_ml;        // running max and sum per partial row
+  int2* own_desc;      // MFMA path: per (sequence, KV head), the sequence's own run
+  int2* pre_desc;      // MFMA path: per (sequence, KV head), its shared-prefix run
+  int64_t rec_own;     // MFMA path: first row of the per-(sequence, head) own-run records
+  int64_t rec_pre;     // ... and of the shared-prefix records
   float scale;
   int B, Hq, Hkv, G, D, bs, Mb, PT, max_parts;
   int NB;  // cache blocks; a block id outside [0, NB) contributes no tokens

@@ -32,15 +32,6 @@ constexpr int kNCT = 4;  // column tiles per wave
 // Chunks are taken in order and made disjoint: chunk n covers q rows
 // [max(q_start[n], end of chunk n-1), max(q_start[n+1], that)), clamped to
 // [0, Tq).  Its rows sit at positions seq_lens[n] - L + i.
-__device__ __forceinline__ int wave_incl_max(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(v, o, 64);
-    if (lane >= o) v = max(v, u);
-  }
-  return v;
-}
-
 __device__ __forceinline__ int block_kvlen(int pos0, int qb, int QB, int rows, int cap) {
   return max(0, min(pos0 + qb * QB + rows, cap));
 }

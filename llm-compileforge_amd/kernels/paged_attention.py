@@ -50,6 +50,7 @@ def paged_attention_tensors(
     partition_tokens: int = DEFAULT_PARTITION_TOKENS,
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    shared_prefix_lens: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Decode attention for a batch held in tensors.
 
@@ -62,6 +63,11 @@ def paged_attention_tensors(
         block_size: tokens per block (must equal k_cache.shape[1]).
         scale: softmax scale, default 1/sqrt(D).
         k_scale, v_scale: dequant scales for float8_e4m3fn caches.
+        shared_prefix_lens: optional int32 [B]; entry b = leading tokens of
+            sequence b held in the same physical blocks as sequence b - 1's
+            (cf_hip.ops.shared_prefix_lens computes it from host tables).
+            Shared blocks are then read once per group of sharers; the
+            result is unchanged (up to summation order).  Trusted as given.
 
     Returns:
         [B, Hq, D] tensor in q's dtype.
@@ -76,6 +82,7 @@ def paged_attention_tensors(
     return _ops.paged_decode(
         q, k_cache, v_cache, block_tables, seq_lens, float(scale), int(block_size),
         k_scale=k_scale, v_scale=v_scale, partition_tokens=partition_tokens, out=out, workspace=workspace,
+        shared_prefix_lens=shared_prefix_lens,
     )
 
 
@@ -141,11 +148,15 @@ def paged_attention(
     for i, t in enumerate(tables):
         host_tables[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
     host_lens = torch.tensor(lens, dtype=torch.int32).pin_memory()
+    # Blocks shared between neighbouring requests (radix-cache prefixes) are
+    # read once per group of sharers.
+    host_shared = torch.tensor(_ops.shared_prefix_lens(tables, lens, block_size), dtype=torch.int32).pin_memory()
     dev_tables = host_tables.to(q.device, non_blocking=True)
     dev_lens = host_lens.to(q.device, non_blocking=True)
+    dev_shared = host_shared.to(q.device, non_blocking=True)
     out = paged_attention_tensors(
         q[: len(rids)], k_cache, v_cache, dev_tables, dev_lens, block_size, scale,
-        k_scale=k_scale, v_scale=v_scale, partition_tokens=partition_tokens,
+        k_scale=k_scale, v_scale=v_scale, partition_tokens=partition_tokens, shared_prefix_lens=dev_shared,
     )
     return {rid: out[i] for i, rid in enumerate(rids)}
 

@@ -13,7 +13,8 @@ Ops:
                       planned hal.paged_attention op
                       (sf-dialect/include/Sf/HALOps.td:184-189).  kwargs:
                       seq_lens, block_size, scale, k_scale, v_scale,
-                      partition_tokens.  Returns [B, Hq, D].
+                      partition_tokens, shared_prefix_lens.  Returns
+                      [B, Hq, D].
   chunked_prefill_attention
                       inputs [query, key_cache, value_cache, block_tables,
                       seq_lens, q_start]; kwargs: block_size, scale,
@@ -101,6 +102,7 @@ class HipBackend(OpExecutor):
             q, k_cache, v_cache, table, seq_lens, block_size, kw.get("scale"),
             k_scale=kw.get("k_scale"), v_scale=kw.get("v_scale"),
             partition_tokens=int(kw.get("partition_tokens", self._partition_tokens)),
+            shared_prefix_lens=kw.get("shared_prefix_lens"),
         )
 
     def _chunked_prefill(self, inputs: list[Any], **kw: Any) -> torch.Tensor:

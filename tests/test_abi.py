@@ -207,3 +207,17 @@ def test_last_error_truncates_safely():
     buf = ctypes.create_string_buffer(8)
     n = _abi.lib().cf_last_error(buf, 8)
     assert n > 8 and len(buf.value) == 7
+
+
+def test_shared_prefix_statement_is_validated():
+    lib = _abi.lib()
+    args = list(_decode_args())
+    for bad, message in ((torch.zeros(2, dtype=torch.int64), "shared_prefix_lens: expected i32"),
+                         (torch.zeros(3, dtype=torch.int32), "shared_prefix_lens has 3 entries")):
+        ds = [_abi.descriptor(t) for t in args]
+        dsh = _abi.descriptor(bad)
+        for d in ds + [dsh]:
+            d.t.device = _abi.SFA_ROCM
+        rc = lib.cf_paged_decode_shared(*(_abi.ref(d) for d in ds[:5]), _abi.ref(dsh), None, None, 0.125, 16, 512,
+                                        _abi.ref(ds[5]), None, 0, None)
+        assert rc == _abi.CF_ERR_INVALID and message in _abi.last_error()

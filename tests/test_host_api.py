@@ -133,3 +133,34 @@ def test_algorithmic_bytes():
     assert ab["unique_kv"] == (16 + 4 + 14) * per_tok
     assert ab["logical"] - ab["unique"] == (50 - 34) * per_tok
     assert ab["tokens"] == 50
+
+
+def test_shared_prefix_lens_matches_token_level_definition():
+    """ops.shared_prefix_lens against a token-by-token statement of sharing:
+    the longest t such that every token x < t of both sequences lies in the
+    same physical block at the same table position."""
+    import random
+
+    from cf_hip.ops import shared_prefix_lens
+
+    rng = random.Random(3)
+    bs = 16
+    for _ in range(300):
+        n = rng.randint(1, 9)
+        pool = iter(range(10**6))
+        tables, lens = [], []
+        prev = []
+        for _b in range(n):
+            keep = rng.randint(0, len(prev)) if prev and rng.random() < 0.7 else 0
+            nblk = rng.randint(max(keep, 1), keep + 6)
+            t = prev[:keep] + [next(pool) for _ in range(nblk - keep)]
+            tables.append(t)
+            lens.append(rng.randint(1, nblk * bs))
+            prev = t
+        got = shared_prefix_lens(tables, lens, bs)
+        assert got[0] == 0
+        for b in range(1, n):
+            t = 0
+            while (t < min(lens[b - 1], lens[b]) and tables[b - 1][t // bs] == tables[b][t // bs]):
+                t += 1
+            assert got[b] == t, (tables[b - 1], tables[b], lens[b - 1], lens[b], got[b], t)
