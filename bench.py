@@ -133,8 +133,7 @@ def bench_mixed(args) -> dict:
             steps_fns[i % len(steps_fns)]()
         torch.cuda.synchronize()
     us = {}
-    for name in ("cf_kv_write_fp8", "cf_decode_mfma", "cf_decode_merge", "cf_prefill_plan", "cf_prefill_mfma",
-                 "cf_prefill_merge"):
+    for name in ("cf_kv_write_fp8", "cf_decode_mfma", "cf_decode_merge", "cf_prefill_plan", "cf_prefill_mfma"):
         ms, n = timer.query(name)
         us[name] = ms / max(n, 1) * 1e3
     timer.reset()

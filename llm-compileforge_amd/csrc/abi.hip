@@ -432,10 +432,9 @@ int32_t cf_prefill_chunk_fp8(const CfTensor* q, const CfTensor* k_cache, const C
     return CF_ERR_UNSUPPORTED;
   }
   if (Tq == 0 || N == 0) return CF_OK;
-  p.QB = prefill_query_block(p.G);
-  p.max_v = (int)(Tq / p.QB + N + 1);
-  CF_CHECK(((int64_t)p.max_v + 1) * ceil_div(vt.size[1] * 16, 32) < (int64_t)INT32_MAX,
-           "query blocks x context tiles overflow int32");
+  p.RB = prefill_rows_per_item(p.G);
+  CF_CHECK((Tq / p.RB + N) * Hkv < (int64_t)INT32_MAX / 2, "too many prefill work items");
+  p.max_items = (int)((Tq / p.RB + N) * Hkv);
   const uint64_t need = prefill_workspace_bytes(Tq, N, Hq, Hkv, D);
   if (workspace == nullptr || workspace_bytes < need) {
     set_error("workspace of %llu bytes needed, %llu given", (unsigned long long)need,

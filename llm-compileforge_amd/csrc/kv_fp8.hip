@@ -131,6 +131,96 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteParams p) {
   }
 }
 
+// 16 consecutive source elements (16-byte aligned) as floats.
+template <int XT>
+__device__ __forceinline__ void load16(const void* src, float* f) {
+  const uint4* s = (const uint4*)src;
+  if constexpr (XT == kF32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 u = s[i];
+      f[4 * i] = u2f(u.x);
+      f[4 * i + 1] = u2f(u.y);
+      f[4 * i + 2] = u2f(u.z);
+      f[4 * i + 3] = u2f(u.w);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 u = s[i];
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (XT == kBF16) {
+          f[8 * i + 2 * j] = f32_from_bf16_bits(w[j] & 0xFFFFu);
+          f[8 * i + 2 * j + 1] = f32_from_bf16_bits(w[j] >> 16);
+        } else {
+          f[8 * i + 2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xFFFFu));
+          f[8 * i + 2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
+        }
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ uint4 pack16(const uint32_t* b) {
+  uint4 r;
+  r.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+  r.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  r.z = b[8] | (b[9] << 8) | (b[10] << 16) | (b[11] << 24);
+  r.w = b[12] | (b[13] << 8) | (b[14] << 16) | (b[15] << 24);
+  return r;
+}
+
+// Paged write into the native layout (block size 16: K tile [bs][D] token
+// rows, V tile [D][bs] channel rows).  One thread per (new token, head,
+// 16-channel piece): 16 K values quantized into one 16-byte store of the
+// token's K row, 16 V values into one byte of each of 16 V channel rows.
+// Codes are the same e4m3_from_f32(x / scale) as kv_write_kernel.
+template <int XT, int ST>
+__global__ __launch_bounds__(256) void kv_write_native_kernel(KvWriteParams p) {
+  using XE = Elem<XT>;
+  constexpr int EB = sizeof(typename XE::T);
+  const int nch = p.D / 16;
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= p.T * p.H * nch) return;
+  const int c = (int)(u % nch), h = (int)((u / nch) % p.H);
+  const int64_t i = u / ((int64_t)nch * p.H);
+  const int64_t sl = ST == kI64 ? ((const int64_t*)p.slots)[i * p.slot_stride]
+                                : (int64_t)((const int32_t*)p.slots)[i * p.slot_stride];
+  if (sl < 0 || sl >= p.NB * 16) return;
+  const int64_t blk = sl >> 4;
+  const int off = (int)(sl & 15);
+  float f[16];
+  uint32_t b[16];
+  load16<XT>((const uint8_t*)p.k_new.base + (i * p.k_new.stride[1] + h * p.k_new.stride[2] + c * 16) * EB, f);
+  const float ks = p.k_scale[h * p.ks_s];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) b[e] = e4m3_from_f32(f[e] / ks);
+  *(uint4*)((uint8_t*)p.k_cache + blk * p.kc_s[0] + h * p.kc_s[2] + off * p.D + c * 16) = pack16(b);
+  load16<XT>((const uint8_t*)p.v_new.base + (i * p.v_new.stride[1] + h * p.v_new.stride[2] + c * 16) * EB, f);
+  const float vs = p.v_scale[h * p.vs_s];
+  uint8_t* vrow = (uint8_t*)p.v_cache + blk * p.vc_s[0] + h * p.vc_s[2] + (c * 16) * 16 + off;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) vrow[e * 16] = e4m3_from_f32(f[e] / vs);
+}
+
+// Whether kv_write_native_kernel applies: native cache layout with block
+// size 16, 16-byte aligned K rows and V channel rows, and new K/V rows whose
+// 16-channel pieces are 16-byte aligned.
+bool kv_write_native_ok(const KvWriteParams& p, int x_dt) {
+  const int eb = x_dt == kF32 ? 4 : 2;
+  if (p.bs != 16 || p.D % 16 != 0) return false;
+  if (p.kc_s[3] != 1 || p.kc_s[1] != p.D || p.vc_s[1] != 1 || p.vc_s[3] != 16) return false;
+  if ((p.kc_s[0] | p.kc_s[2] | p.vc_s[0] | p.vc_s[2]) & 15) return false;
+  if (((uintptr_t)p.k_cache | (uintptr_t)p.v_cache) & 15) return false;
+  for (const Rank4* x : {&p.k_new, &p.v_new}) {
+    if (x->stride[3] != 1 || ((uintptr_t)x->base & 15)) return false;
+    if (((x->stride[1] * eb) | (x->stride[2] * eb)) & 15) return false;
+  }
+  return true;
+}
+
 int grid_for(int64_t n) {
   int64_t g = (n + 255) / 256;
   if (g > 65536) g = 65536;
@@ -198,6 +288,23 @@ int32_t launch_dequantize(const Rank4& q, const float* scales, int64_t s_stride,
 
 int32_t launch_kv_write_fp8(const KvWriteParams& p, int x_dt, int slot_dt, hipStream_t stream) {
   if (p.T == 0) return CF_OK;
+  if (kv_write_native_ok(p, x_dt)) {
+    const dim3 grid((unsigned)ceil_div(p.T * p.H * (p.D / 16), 256));
+    ProfileScope prof("cf_kv_write_fp8", stream);
+#define CF_KVN(XT, ST) hipLaunchKernelGGL((kv_write_native_kernel<XT, ST>), grid, dim3(256), 0, stream, p)
+    switch (x_dt * 8 + (slot_dt == kI64 ? 1 : 0)) {
+      case kF32 * 8: CF_KVN(kF32, kI32); break;
+      case kF32 * 8 + 1: CF_KVN(kF32, kI64); break;
+      case kF16 * 8: CF_KVN(kF16, kI32); break;
+      case kF16 * 8 + 1: CF_KVN(kF16, kI64); break;
+      case kBF16 * 8: CF_KVN(kBF16, kI32); break;
+      case kBF16 * 8 + 1: CF_KVN(kBF16, kI64); break;
+      default: set_error("kv_write: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
+    }
+#undef CF_KVN
+    CF_HIP_CHECK(hipGetLastError());
+    return CF_OK;
+  }
   const dim3 grid((unsigned)p.T);
   const int threads = p.H * p.D >= 256 ? 256 : 64 * (int)ceil_div(p.H * p.D, 64);
   ProfileScope prof("cf_kv_write_fp8", stream);

@@ -3,20 +3,35 @@
 // A chunk of L new query rows whose sequence now holds S tokens (its own
 // K/V already written to the cache) puts row i at position S - L + i; the
 // row attends to cache positions [0, S - L + i] (causal inside the chunk,
-// everything before it).  This is the reference's decode semantics
+// everything before it), read through the chunk's block table up to
+// Mb * 16 tokens.  This is the reference's decode semantics
 // (kernels/paged_attention.py:21-73) applied per row with the length cut
 // to the row's position, the rule the reference's chunked prefill
 // (runtime/src/engine/scheduler.rs:178-226) implies.
 //
-// Shape of the work.  The 16 columns of an MFMA tile hold query columns
-// (row, query head): 16/G rows x the G query heads of one KV head.  A wave
-// carries NCT = 4 such column tiles (a "query block" of QB = 64/G rows), so
-// every 32-token K/V tile it loads and converts feeds 4 x 16 MFMAs.  Each
-// (query block, KV head) is one run over the tiles up to its last row's
-// position; runs are laid out in a tile stream (KV head, query block, tile)
-// and split evenly over the resident waves exactly like the decode kernel
-// (decode_mfma.hip), with (m, l, o) partials for runs split between waves,
-// merged by prefill_merge_kernel.
+// Shape of the work.  A work item is (chunk n, KV head h, row block rb):
+// RB = 128 / G query rows of chunk n times the G query heads of h, i.e.
+// 128 query columns (column c: row c / G, head c % G).  One workgroup of
+// four waves takes an item; wave w owns columns [32 w, 32 w + 32) as two
+// 16-column tiles of v_mfma_f32_16x16x32_{bf16,f16}.  The item's K/V are
+// walked in 32-token tiles (two 16-token blocks).  Each tile is read from
+// HBM / L2 once per workgroup, converted (e4m3 K -> bf16, e4m3 V -> fp16,
+// both exact) and written to LDS in MFMA operand order: an LDS entry is the
+// 16 bytes one lane feeds one MFMA, entries of one MFMA are consecutive, so
+// every operand read is a conflict-free ds_read_b128.  Two LDS buffers and
+// two register stages: while tile j is computed from LDS, tile j + 1 goes
+// from registers to the other buffer and tile j + 2 is loading.
+//
+// Per tile and column tile the math is the decode kernel's (decode_mfma.hip):
+// S^T = K Q^T as two 16-token MFMA chains, online softmax in log2 units
+// with lazy rescaling, O^T += V^T P^T; the K-row order inside the tile
+// makes each lane's scores exactly the P^T operand it feeds.
+//
+// Items come from a queue the plan kernel sorts longest first (counting
+// sort on the tile count), so the persistent workgroups finish together
+// without splitting an item: there are no partials and no merge pass.
+#include <type_traits>
+
 #include "cf_device.hpp"
 #include "cf_host.hpp"
 #include "mfma_tile.hpp"
@@ -26,430 +41,412 @@ namespace cf {
 
 namespace {
 
-constexpr int kNCT = 4;  // column tiles per wave
+constexpr int kCols = 128;        // query columns per work item
+constexpr int kPlanThreads = 1024;
+constexpr int kCostBins = 2048;   // tile counts at or above share the last bin
 
-// ---- plan: one wave lists the query blocks and their tile offsets ---------
+__device__ __forceinline__ int item_kvlen(int pos0, int rb, int RB, int L, int cap) {
+  const int rows = min(RB, L - rb * RB);
+  return max(0, min(pos0 + rb * RB + rows, cap));
+}
+
+// ---- plan: chunk rows, work items, longest-first order -------------------
 // Chunks are taken in order and made disjoint: chunk n covers q rows
 // [max(q_start[n], end of chunk n-1), max(q_start[n+1], that)), clamped to
 // [0, Tq).  Its rows sit at positions seq_lens[n] - L + i.
-__device__ __forceinline__ int block_kvlen(int pos0, int qb, int QB, int rows, int cap) {
-  return max(0, min(pos0 + qb * QB + rows, cap));
-}
-
-__global__ __launch_bounds__(64) void prefill_plan_kernel(PrefillParams p) {
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillParams p) {
+  __shared__ int hist[kCostBins];
+  __shared__ int wave_tot[kPlanThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cap = p.Mb * 16;
-  int vbase = 0, tbase = 0, rend = 0;
-  for (int n0 = 0; n0 < p.N; n0 += 64) {
-    const int n = n0 + lane;
-    int a = 0, b = 0, S = 0;
-    if (n < p.N) {
-      a = min(max(p.q_start[(int64_t)n * p.qs_s], 0), p.Tq);
-      b = min(max(p.q_start[(int64_t)(n + 1) * p.qs_s], 0), p.Tq);
-      S = p.seq_lens[(int64_t)n * p.sl_s];
-    }
-    const int row1 = max(wave_incl_max(max(a, b), lane), rend);
-    int prev_end = __shfl_up(row1, 1, 64);
-    if (lane == 0) prev_end = rend;
-    const int row0 = n < p.N ? max(a, prev_end) : row1;
-    const int L = n < p.N ? row1 - row0 : 0;
-    const int pos0 = S - L;
-    const int nqb = (L + p.QB - 1) / p.QB;
-    int ctiles = 0;
-    for (int qb = 0; qb < nqb; ++qb) {
-      const int rows = min(p.QB, L - qb * p.QB);
-      ctiles += (block_kvlen(pos0, qb, p.QB, rows, cap) + 31) >> 5;
-    }
-    const int incl_v = wave_incl_scan(nqb, lane);
-    const int incl_t = wave_incl_scan(ctiles, lane);
-    int run = tbase + incl_t - ctiles;
-    for (int qb = 0; qb < nqb; ++qb) {
-      const int v = vbase + incl_v - nqb + qb;
-      const int rows = min(p.QB, L - qb * p.QB);
-      const int kvlen = block_kvlen(pos0, qb, p.QB, rows, cap);
-      if (v < p.max_v) {
-        p.vseq[v] = make_int4(n, row0 + qb * p.QB, rows, pos0 + qb * p.QB);
-        p.vtiles[v] = run;
-        // query blocks that read nothing get zero rows from the merge kernel
-        if (kvlen == 0)
-          for (int h = 0; h < p.Hkv; ++h) p.merge_desc[(int64_t)v * p.Hkv + h] = make_int2(-1, 0);
+  if (wave == 0) {
+    // chunk rows, and in .w the row blocks of the chunks before this one
+    int rend = 0, nrb_run = 0;
+    for (int n0 = 0; n0 < p.N; n0 += 64) {
+      const int n = n0 + lane;
+      int a = 0, b = 0, S = 0;
+      if (n < p.N) {
+        a = min(max(p.q_start[(int64_t)n * p.qs_s], 0), p.Tq);
+        b = min(max(p.q_start[(int64_t)(n + 1) * p.qs_s], 0), p.Tq);
+        S = p.seq_lens[(int64_t)n * p.sl_s];
       }
-      run += (kvlen + 31) >> 5;
+      const int row1 = max(wave_incl_max(max(a, b), lane), rend);
+      int prev_end = __shfl_up(row1, 1, 64);
+      if (lane == 0) prev_end = rend;
+      const int row0 = n < p.N ? max(a, prev_end) : row1;
+      const int L = n < p.N ? row1 - row0 : 0;
+      const int nrb = (L + p.RB - 1) / p.RB;
+      const int incl = wave_incl_scan(nrb, lane) + nrb_run;
+      if (n < p.N) p.chunks[n] = make_int4(row0, L, S - L, incl - nrb);
+      rend = __shfl(row1, 63, 64);
+      nrb_run = __shfl(incl, 63, 64);
     }
-    vbase += __shfl(incl_v, 63, 64);
-    tbase += __shfl(incl_t, 63, 64);
-    rend = __shfl(row1, 63, 64);
+    if (lane == 0) wave_tot[0] = nrb_run;
   }
-  if (lane == 0) {
-    // max_v bounds the block count of disjoint chunks; the check is a guard
-    const bool fits = vbase <= p.max_v;
-    if (fits) p.vtiles[vbase] = tbase;
-    p.header[0] = fits ? vbase : 0;
-    p.header[1] = fits ? tbase : 0;
+  for (int i = tid; i < kCostBins; i += kPlanThreads) hist[i] = 0;
+  __syncthreads();
+  const int nblocks = wave_tot[0];  // row blocks of all chunks
+  __syncthreads();
+  // Row block f (flattened over chunks): its chunk by binary search on .w;
+  // items (f, h) for every KV head.  Bin kCostBins-1-tiles puts the longest
+  // items first.
+  for (int f = tid; f < nblocks; f += kPlanThreads) {
+    int lo = 0, hi = p.N - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (p.chunks[mid].w <= f) lo = mid;
+      else hi = mid - 1;
+    }
+    const int4 c = p.chunks[lo];
+    const int tiles = (item_kvlen(c.z, f - c.w, p.RB, c.y, cap) + 31) >> 5;
+    atomicAdd(&hist[kCostBins - 1 - min(tiles, kCostBins - 1)], p.Hkv);
+  }
+  __syncthreads();
+  // Exclusive scan of the bins (two per thread).
+  const int h0 = hist[2 * tid], h1 = hist[2 * tid + 1];
+  const int incl = wave_incl_scan(h0 + h1, lane);
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wave_tot[w];
+  const int excl = base + incl - (h0 + h1);
+  const int total = base + incl;  // inclusive through this thread's bins
+  __syncthreads();
+  hist[2 * tid] = excl;
+  hist[2 * tid + 1] = excl + h0;
+  __syncthreads();
+  for (int f = tid; f < nblocks; f += kPlanThreads) {
+    int lo = 0, hi = p.N - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (p.chunks[mid].w <= f) lo = mid;
+      else hi = mid - 1;
+    }
+    const int4 c = p.chunks[lo];
+    const int rb = f - c.w;
+    const int tiles = (item_kvlen(c.z, rb, p.RB, c.y, cap) + 31) >> 5;
+    const int at = atomicAdd(&hist[kCostBins - 1 - min(tiles, kCostBins - 1)], p.Hkv);
+    for (int h = 0; h < p.Hkv; ++h)
+      if (at + h < p.max_items) p.items[at + h] = make_int4(lo, rb, h, tiles);
+  }
+  if (tid == kPlanThreads - 1) {
+    p.header[0] = min(total, p.max_items);  // the last thread's inclusive sum: all items
+    p.header[1] = 0;                        // queue counter
   }
 }
 
-struct PIndex {
-  const int32_t* __restrict__ tables;
-  const int4* __restrict__ vseq;
-  const int* __restrict__ vtiles;
-  const float* __restrict__ kscale;
-  const float* __restrict__ vscale;
+// ---- the work-item kernel ---------------------------------------------------
+
+template <int KT, int D>
+struct Geo {
+  static constexpr int KB = KvTraits<KT>::kBytes;
+  static constexpr int NC = D / 32;             // QK MFMA steps per chain
+  static constexpr int NV = D / 16;             // PV MFMAs per column tile
+  static constexpr int KENT = 2 * NC * 64;      // K operand entries (16 B) per tile
+  static constexpr int VENT = NV * 64;          // V operand entries per tile
+  static constexpr int KUPL = D / 4 * KB / 16;  // 16-byte K loads per (chain, lane)
+  static constexpr int KU = 2 * 64 * KUPL;      // K loads per tile
+  static constexpr int VPER = KB;               // 16-byte loads per channel row of a block (16 tokens)
+  static constexpr int VU = 2 * D * VPER;       // V loads per tile
+  static constexpr int KPT = (KU + 255) / 256;  // per thread
+  static constexpr int VPT = (VU + 255) / 256;
 };
 
-struct PCoord {
-  int h, v, j;
-  int n, row0, rows, pos0;  // query block: chunk, first row, rows, position of the first row
-  int kvlen, nt;            // cache tokens the block reads, and their tiles
-  int blkA, blkB;
+struct TileIds {
+  int a, b;     // physical blocks (block 0 stands in for an invalid id)
+  bool va, vb;  // ids valid
 };
 
-__device__ __forceinline__ void set_block(const PrefillParams& p, const PIndex& ix, PCoord& c) {
-  const int4 e = ix.vseq[c.v];
-  c.n = e.x;
-  c.row0 = e.y;
-  c.rows = e.z;
-  c.pos0 = e.w;
-  c.kvlen = block_kvlen(c.pos0, 0, 0, c.rows, p.Mb * 16);
-  c.nt = (c.kvlen + 31) >> 5;
+__device__ __forceinline__ TileIds tile_ids(const PrefillParams& p, const int32_t* __restrict__ tables, int n,
+                                            int j, int kvlen) {
+  TileIds t;
+  const int nblk = (kvlen + 15) >> 4;
+  const int ia = tables[(int64_t)n * p.t_sb + (int64_t)(2 * j) * p.t_sm];
+  const int ib = 2 * j + 1 < nblk ? tables[(int64_t)n * p.t_sb + (int64_t)(2 * j + 1) * p.t_sm] : -1;
+  t.va = ia >= 0 && ia < p.NB;
+  t.vb = ib >= 0 && ib < p.NB;
+  t.a = t.va ? ia : 0;
+  t.b = t.vb ? ib : 0;
+  return t;
 }
 
-__device__ __forceinline__ int checked_block(const PrefillParams& p, const PIndex& ix, int n, int jb) {
-  const int id = ix.tables[(int64_t)n * p.t_sb + (int64_t)jb * p.t_sm];
-  return (id >= 0 && id < p.NB) ? id : -1;
+// Global loads of one K/V tile into registers (16 bytes each).
+template <int KT, int D>
+__device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillParams& p, const TileIds& t, int h,
+                                           int tid) {
+  using Gm = Geo<KT, D>;
+  const uint8_t* kbase = (const uint8_t*)p.k;
+  const uint8_t* vbase = (const uint8_t*)p.v;
+#pragma unroll
+  for (int i = 0; i < Gm::KPT; ++i) {
+    const int u = tid + 256 * i;
+    if (u < Gm::KU) {
+      const int s = u / (64 * Gm::KUPL), rem = u % (64 * Gm::KUPL);
+      const int lane = rem / Gm::KUPL, cp = rem % Gm::KUPL;
+      const int li = lane & 15, lq = lane >> 4;
+      const int row = ((8 * (li >> 2) + (li & 3)) & 15) + 4 * s;
+      const int blk = li < 8 ? t.a : t.b;
+      const int64_t off =
+          ((int64_t)blk * p.k_s[0] + (int64_t)h * p.k_s[2] + row * D + lq * (D / 4)) * Gm::KB + cp * 16;
+      kr[i] = *(const uint4*)(kbase + off);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < Gm::VPT; ++i) {
+    const int u = tid + 256 * i;
+    if (u < Gm::VU) {
+      // 16 bytes of channel d of block X: all 16 tokens (e4m3) or half of them (bf16)
+      const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
+      const int d = rem / Gm::VPER, part = rem % Gm::VPER;
+      const int blk = X ? t.b : t.a;
+      const int64_t off = ((int64_t)blk * p.v_s[0] + (int64_t)h * p.v_s[2] + d * 16) * Gm::KB + part * 16;
+      vr[i] = *(const uint4*)(vbase + off);
+    }
+  }
 }
 
-__device__ __forceinline__ void fetch_ids(const PrefillParams& p, const PIndex& ix, PCoord& c) {
-  const int nblk = (c.kvlen + 15) >> 4;
-  c.blkA = checked_block(p, ix, c.n, 2 * c.j);
-  c.blkB = 2 * c.j + 1 < nblk ? checked_block(p, ix, c.n, 2 * c.j + 1) : -1;
-}
-
-__device__ __forceinline__ PCoord advance(const PrefillParams& p, const PIndex& ix, PCoord c, int nv) {
-  if (c.j + 1 < c.nt) {
-    c.j += 1;
-  } else {
-    c.j = 0;
-    do {
-      c.v += 1;
-      if (c.v == nv) {
-        c.v = 0;
-        c.h += 1;
+// Converts the staged registers and writes them in operand order: K entry
+// (chain s, step c, lane) = the 8 channels lane (li, lq) feeds step c of
+// chain s; V entry (step t, lane) = channel 16 t + li, tokens 8 lq .. 8 lq + 7.
+// V tokens at or past `valid` (tile-relative) or in an invalid block become
+// zero (cache slots there may hold any bits, NaN codes included).
+template <int KT, int D>
+__device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const uint4* vr, const TileIds& t,
+                                            int valid, int tid) {
+  using Gm = Geo<KT, D>;
+#pragma unroll
+  for (int i = 0; i < Gm::KPT; ++i) {
+    const int u = tid + 256 * i;
+    if (u < Gm::KU) {
+      const int s = u / (64 * Gm::KUPL), rem = u % (64 * Gm::KUPL);
+      const int lane = rem / Gm::KUPL, cp = rem % Gm::KUPL;
+      if constexpr (KT == kE4M3) {
+        lds[(s * Gm::NC + 2 * cp) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_bf16(kr[i].x, kr[i].y));
+        lds[(s * Gm::NC + 2 * cp + 1) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_bf16(kr[i].z, kr[i].w));
+      } else {
+        lds[(s * Gm::NC + cp) * 64 + lane] = kr[i];
       }
-      set_block(p, ix, c);
-    } while (c.nt == 0);
+    }
   }
-  fetch_ids(p, ix, c);
-  return c;
-}
-
-// Query block v holding tile r (0 <= r < Tb) of a head: largest v with
-// vtiles[v] <= r (binary search, wave-uniform).
-__device__ __forceinline__ int find_block(const PIndex& ix, int nv, int r) {
-  int lo = 0, hi = nv - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (ix.vtiles[mid] <= r) lo = mid;
-    else hi = mid - 1;
-  }
-  return lo;
-}
-
-template <int D, int G>
-__device__ __forceinline__ void load_q_block(bf16x8_t (*qop)[D / 32], const PrefillParams& p, const PCoord& c,
-                                             int li, int lq) {
-  constexpr int NC = D / 32;
-  constexpr int RPT = 16 / G;  // rows per column tile
+  uint4* vl = lds + Gm::KENT;
 #pragma unroll
-  for (int ct = 0; ct < kNCT; ++ct) {
-    const int t = ct * RPT + li / G;
-    if (t < c.rows) {
-      const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(c.row0 + t) * p.q_sr +
-                             (int64_t)(c.h * G + li % G) * p.q_sh + lq * (D / 4);
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc) qop[ct][cc] = as_bf16x8(*(const uint4*)(qrow + 8 * cc));
-    } else {
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc) qop[ct][cc] = as_bf16x8(make_uint4(0, 0, 0, 0));
+  for (int i = 0; i < Gm::VPT; ++i) {
+    const int u = tid + 256 * i;
+    if (u < Gm::VU) {
+      const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
+      const int d = rem / Gm::VPER, part = rem % Gm::VPER;
+      const bool ok = X ? t.vb : t.va;
+      const int li = d & 15, tt = d >> 4;
+      if constexpr (KT == kE4M3) {
+        const int n0 = ok ? valid - 16 * X : 0;  // valid tokens among this load's 16
+        const uint2 lo = keep_bytes(make_uint2(vr[i].x, vr[i].y), n0);
+        const uint2 hi = keep_bytes(make_uint2(vr[i].z, vr[i].w), n0 - 8);
+        vl[tt * 64 + 32 * X + li] = __builtin_bit_cast(uint4, e4m3x8_to_f16(lo.x, lo.y));
+        vl[tt * 64 + 32 * X + 16 + li] = __builtin_bit_cast(uint4, e4m3x8_to_f16(hi.x, hi.y));
+      } else {
+        const int n0 = ok ? valid - 16 * X - 8 * part : 0;
+        vl[tt * 64 + 32 * X + 16 * part + li] = mask_tokens(vr[i], n0);
+      }
     }
   }
 }
-
-template <int D>
-struct PRun {
-  float m[kNCT], l[kNCT];
-  f32x4_t o[kNCT][D / 16];
-  int j0;
-  __device__ __forceinline__ void reset(int j) {
-#pragma unroll
-    for (int ct = 0; ct < kNCT; ++ct) {
-      m[ct] = -INFINITY;
-      l[ct] = 0.0f;
-#pragma unroll
-      for (int t = 0; t < D / 16; ++t) o[ct][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    j0 = j;
-  }
-};
 
 template <int KT, int D, int G>
-__device__ __forceinline__ void prefill_tile(PRun<D>& st, TileRegs<KT, D>& r, const PCoord& c,
-                                             const bf16x8_t (*qop)[D / 32], float qk_scale, int li, int lq) {
-  constexpr int NC = D / 32;
-  constexpr int NV = D / 16;
-  constexpr int RPT = 16 / G;
-  // tokens past the block's cache length may hold any bits: zero their V
-  const bool edge = c.kvlen - 32 * c.j < 32 || c.blkA < 0 || c.blkB < 0;
-  const bool blk_ok = (lq < 2 ? c.blkA : c.blkB) >= 0;
-  const int nvalid = blk_ok ? c.kvlen - 32 * c.j - 8 * lq : 0;  // valid of this lane's 8 tokens
-  if (edge) {
-#pragma unroll
-    for (int t = 0; t < NV; ++t) r.v[t] = mask_tokens(r.v[t], nvalid);
-  }
-  // operands converted once for all column tiles
-  bf16x8_t k1[NC], k2[NC];
-#pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
-    k1[cc] = k_operand<KT>(r.k1, cc);
-    k2[cc] = k_operand<KT>(r.k2, cc);
-  }
-  using VOp = typename std::conditional<KT == kE4M3, f16x8_t, bf16x8_t>::type;
-  VOp vop[NV];
-#pragma unroll
-  for (int t = 0; t < NV; ++t) {
-    if constexpr (KT == kE4M3) vop[t] = e4m3x8_to_f16(r.v[t].x, r.v[t].y);
-    else vop[t] = as_bf16x8(r.v[t]);
-  }
-  const int kp0 = 32 * c.j + 8 * lq;  // cache position of this lane's first token
-#pragma unroll
-  for (int ct = 0; ct < kNCT; ++ct) {
-    f32x4_t s1 = {0.0f, 0.0f, 0.0f, 0.0f}, s2 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1[cc], qop[ct][cc], s1, 0, 0, 0);
-      s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2[cc], qop[ct][cc], s2, 0, 0, 0);
-    }
-    float sc[8];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      sc[v] = s1[v] * qk_scale;
-      sc[4 + v] = s2[v] * qk_scale;
-    }
-    // causal: column li's row sits at position qpos; only tiles reaching
-    // past the column tile's first row (or the cache end) need masks
-    const int qmin = c.pos0 + ct * RPT;
-    if (edge || 32 * c.j + 31 > qmin) {
-      const int qpos = qmin + li / G;
-#pragma unroll
-      for (int v = 0; v < 8; ++v)
-        if (v >= nvalid || kp0 + v > qpos) sc[v] = -INFINITY;
-    }
-    float mt = sc[0];
-#pragma unroll
-    for (int v = 1; v < 8; ++v) mt = fmaxf(mt, sc[v]);
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    if (__any(mt > st.m[ct] + 8.0f)) {
-      const float mnew = mt > st.m[ct] + 8.0f ? mt : st.m[ct];
-      const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m[ct] - mnew);
-      st.l[ct] *= alpha;
-#pragma unroll
-      for (int t = 0; t < NV; ++t) st.o[ct][t] = st.o[ct][t] * alpha;
-      st.m[ct] = mnew;
-    }
-    float pr[8];
-    float psum = 0.0f;
-    const bool live = st.m[ct] != -INFINITY;
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      pr[v] = live ? __builtin_amdgcn_exp2f(sc[v] - st.m[ct]) : 0.0f;
-      psum += pr[v];
-    }
-    st.l[ct] += psum;
-    if constexpr (KT == kE4M3) {
-      f16x8_t pop;
-#pragma unroll
-      for (int v = 0; v < 8; ++v) pop[v] = (_Float16)pr[v];
-#pragma unroll
-      for (int t = 0; t < NV; ++t)
-        st.o[ct][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[t], pop, st.o[ct][t], 0, 0, 0);
-    } else {
-      bf16x8_t pop, plo;
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const __bf16 hi = (__bf16)pr[v];
-        pop[v] = hi;
-        plo[v] = (__bf16)(pr[v] - (float)hi);
-      }
-#pragma unroll
-      for (int t = 0; t < NV; ++t) {
-        st.o[ct][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[t], pop, st.o[ct][t], 0, 0, 0);
-        st.o[ct][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[t], plo, st.o[ct][t], 0, 0, 0);
-      }
-    }
-  }
-}
-
-template <int D, int G>
-__device__ __forceinline__ void prefill_flush(const PrefillParams& p, const PIndex& ix, const PRun<D>& st,
-                                              const PCoord& c, int64_t tau, int64_t chunk, int w, bool first_run,
-                                              int lane) {
-  constexpr int NV = D / 16;
-  constexpr int RPT = 16 / G;
+__global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, const int32_t* __restrict__ tables,
+                                                              const int4* __restrict__ items,
+                                                              const int4* __restrict__ chunks, int* header,
+                                                              const float* __restrict__ kscale,
+                                                              const float* __restrict__ vscale) {
+  using Gm = Geo<KT, D>;
+  constexpr int NC = Gm::NC, NV = Gm::NV;
+  constexpr int RB = kCols / G;
+  __shared__ uint4 lds[2][Gm::KENT + Gm::VENT];
+  __shared__ int s_item;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = uniform(tid >> 6);
   const int li = lane & 15, lq = lane >> 4;
-  const float vs = ix.vscale ? ix.vscale[c.h * p.vs_s] : 1.0f;
-  const bool complete = st.j0 == 0 && c.j == c.nt - 1;
-  if (st.j0 == 0 && lane == 0) {
-    int2 desc = make_int2(0, 0);
-    if (!complete) {
-      const int64_t s_tile = tau - c.j;
-      const int w1 = (int)(s_tile / chunk);
-      const int w2 = (int)((s_tile + c.nt - 1) / chunk);
-      desc = make_int2(w1 * 2 + ((int64_t)w1 * chunk < s_tile ? 1 : 0), w2 - w1 + 1);
+  const int n_items = header[0];
+  const int cap = p.Mb * 16;
+
+  for (;;) {
+    if (tid == 0) s_item = atomicAdd(&header[1], 1);
+    __syncthreads();
+    const int it = uniform(s_item);
+    __syncthreads();
+    if (it >= n_items) break;
+    const int4 item = items[it];
+    const int n = uniform(item.x), rb = uniform(item.y), h = uniform(item.z), nt = uniform(item.w);
+    const int4 ch = chunks[n];
+    const int row0 = uniform(ch.x + rb * RB);
+    const int rows = uniform(min(RB, ch.y - rb * RB));
+    const int pos0 = uniform(ch.z + rb * RB);
+    const int kvlen = uniform(max(0, min(pos0 + rows, cap)));
+
+    // This wave's columns: tile k, column li -> item column 32 wave + 16 k + li.
+    bf16x8_t qop[2][NC];
+    int lim[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int col = 32 * wave + 16 * k + li;
+      const int r = col / G, g = col % G;
+      const bool used = r < rows;
+      lim[k] = used ? max(0, min(pos0 + r + 1, cap)) : 0;
+      const int rr = used ? r : 0;
+      const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(row0 + rr) * p.q_sr +
+                             (int64_t)(h * G + g) * p.q_sh + lq * (D / 4);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) qop[k][c] = as_bf16x8(*(const uint4*)(qrow + 8 * c));
     }
-    p.merge_desc[(int64_t)c.v * p.Hkv + c.h] = desc;
-  }
-  const int64_t slot = (int64_t)w * 2 + (first_run ? 0 : 1);
+    // tokens every column / some column of this wave may see
+    int lmin = min(lim[0], lim[1]), lmax = max(lim[0], lim[1]);
 #pragma unroll
-  for (int ct = 0; ct < kNCT; ++ct) {
-    float lt = st.l[ct] + __shfl_xor(st.l[ct], 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
-    const int t = ct * RPT + li / G;
-    if (complete) {
-      if (t < c.rows) {
-        const float inv = lt > 0.0f ? vs / lt : 0.0f;
-        uint16_t* orow = (uint16_t*)p.out + (int64_t)(c.row0 + t) * p.o_sr + (int64_t)(c.h * G + li % G) * p.o_sh +
-                         4 * lq;
+    for (int o = 32; o > 0; o >>= 1) {
+      lmin = min(lmin, __shfl_xor(lmin, o, 64));
+      lmax = max(lmax, __shfl_xor(lmax, o, 64));
+    }
+    lmin = uniform(lmin);
+    lmax = uniform(lmax);
+    const float qk_scale = p.scale * (kscale ? kscale[h * p.ks_s] : 1.0f) * kLog2e;
+
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    f32x4_t o[2][NV];
 #pragma unroll
-        for (int tt = 0; tt < NV; ++tt) {
-          uint2 packed;
-          packed.x = (uint32_t)bf16_bits_from_f32(st.o[ct][tt][0] * inv) |
-                     ((uint32_t)bf16_bits_from_f32(st.o[ct][tt][1] * inv) << 16);
-          packed.y = (uint32_t)bf16_bits_from_f32(st.o[ct][tt][2] * inv) |
-                     ((uint32_t)bf16_bits_from_f32(st.o[ct][tt][3] * inv) << 16);
-          *(uint2*)(orow + 16 * tt) = packed;
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int t = 0; t < NV; ++t) o[k][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // K/V registers of two tiles in flight (kr[P], vr[P]) and the block ids
+    // of tiles j .. j + 3: tile j + 2 loads while tile j is computed and
+    // tile j + 1 goes from registers to LDS.
+    uint4 kr[2][Gm::KPT], vr[2][Gm::VPT];
+    TileIds id0 = tile_ids(p, tables, n, 0, kvlen);
+    TileIds id1 = nt > 1 ? tile_ids(p, tables, n, 1, kvlen) : id0;
+    TileIds id2 = nt > 2 ? tile_ids(p, tables, n, 2, kvlen) : id1;
+    if (nt > 0) stage_load<KT, D>(kr[0], vr[0], p, id0, h, tid);
+    if (nt > 1) stage_load<KT, D>(kr[1], vr[1], p, id1, h, tid);
+    if (nt > 0) stage_write<KT, D>(lds[0], kr[0], vr[0], id0, kvlen, tid);
+    __syncthreads();
+
+    auto step = [&](auto par, int j) {
+      constexpr int P = decltype(par)::value;
+      if (j + 2 < nt) stage_load<KT, D>(kr[P], vr[P], p, id2, h, tid);
+      const TileIds id3 = j + 3 < nt ? tile_ids(p, tables, n, j + 3, kvlen) : id2;
+      if (32 * j < lmax) {
+        const uint4* kl = lds[P];
+        const uint4* vl = kl + Gm::KENT;
+        bf16x8_t a1[NC], a2[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          a1[c] = as_bf16x8(kl[c * 64 + lane]);
+          a2[c] = as_bf16x8(kl[(NC + c) * 64 + lane]);
+        }
+        const bool edge = 32 * j + 32 > lmin || !id0.va || !id0.vb;
+        const bool blk_ok = lq < 2 ? id0.va : id0.vb;
+        const int tok0 = 32 * j + 8 * lq;
+        using POp = typename std::conditional<KT == kE4M3, f16x8_t, bf16x8_t>::type;
+        POp pop[2], plo[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          f32x4_t s1 = {0.0f, 0.0f, 0.0f, 0.0f}, s2 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[c], qop[k][c], s1, 0, 0, 0);
+            s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[c], qop[k][c], s2, 0, 0, 0);
+          }
+          // lane (li, lq): s1[v] -> token tok0 + v, s2[v] -> token tok0 + 4 + v
+          float sc[8];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            sc[v] = s1[v] * qk_scale;
+            sc[4 + v] = s2[v] * qk_scale;
+          }
+          if (edge) {
+            const int nvalid = blk_ok ? lim[k] - tok0 : 0;
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+              if (v >= nvalid) sc[v] = -INFINITY;
+          }
+          float mt = sc[0];
+#pragma unroll
+          for (int v = 1; v < 8; ++v) mt = fmaxf(mt, sc[v]);
+          mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+          mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+          // lazy rescale: the running max moves only when a score passes it
+          // by more than 8 (log2 units), so p <= 256
+          if (__any(mt > m[k] + 8.0f)) {
+            const float mnew = mt > m[k] + 8.0f ? mt : m[k];
+            const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[k] - mnew);
+            l[k] *= alpha;
+#pragma unroll
+            for (int t = 0; t < NV; ++t) o[k][t] = o[k][t] * alpha;
+            m[k] = mnew;
+          }
+          const bool live = m[k] != -INFINITY;
+          float psum = 0.0f;
+#pragma unroll
+          for (int v = 0; v < 8; ++v) {
+            const float pv = live ? __builtin_amdgcn_exp2f(sc[v] - m[k]) : 0.0f;
+            psum += pv;
+            if constexpr (KT == kE4M3) {
+              pop[k][v] = (_Float16)pv;
+            } else {
+              const __bf16 hi = (__bf16)pv;
+              pop[k][v] = hi;
+              plo[k][v] = (__bf16)(pv - (float)hi);
+            }
+          }
+          l[k] += psum;
+        }
+        // ---- O^T += V^T P^T ------------------------------------------------
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+          const uint4 vraw = vl[t * 64 + lane];
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            if constexpr (KT == kE4M3) {
+              o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, vraw), pop[k], o[k][t],
+                                                               0, 0, 0);
+            } else {
+              const bf16x8_t vop = as_bf16x8(vraw);
+              o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[k], o[k][t], 0, 0, 0);
+              o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo[k], o[k][t], 0, 0, 0);
+            }
+          }
         }
       }
-    } else {
-      const int col = ct * 16 + li;
-      float* os = p.ws_o + (slot * (16 * kNCT) + col) * D + 4 * lq;
+      if (j + 1 < nt) stage_write<KT, D>(lds[1 - P], kr[1 - P], vr[1 - P], id1, kvlen - 32 * (j + 1), tid);
+      __syncthreads();
+      id0 = id1;
+      id1 = id2;
+      id2 = id3;
+    };
+    for (int j = 0; j < nt; j += 2) {
+      step(std::integral_constant<int, 0>{}, j);
+      if (j + 1 < nt) step(std::integral_constant<int, 1>{}, j + 1);
+    }
+
+    // ---- normalized output --------------------------------------------------
+    const float vs = vscale ? vscale[h * p.vs_s] : 1.0f;
 #pragma unroll
-      for (int tt = 0; tt < NV; ++tt)
-        *(float4*)(os + 16 * tt) = make_float4(st.o[ct][tt][0] * vs, st.o[ct][tt][1] * vs, st.o[ct][tt][2] * vs,
-                                               st.o[ct][tt][3] * vs);
-      if (lq == 0) {
-        p.ws_ml[(slot * (16 * kNCT) + col) * 2] = st.m[ct] == -INFINITY ? -INFINITY : st.m[ct] * (1.0f / kLog2e);
-        p.ws_ml[(slot * (16 * kNCT) + col) * 2 + 1] = lt;
+    for (int k = 0; k < 2; ++k) {
+      float lt = l[k] + __shfl_xor(l[k], 16, 64);
+      lt += __shfl_xor(lt, 32, 64);
+      const int col = 32 * wave + 16 * k + li;
+      const int r = col / G, g = col % G;
+      if (r < rows) {
+        const float inv = lt > 0.0f ? vs / lt : 0.0f;
+        uint16_t* orow = (uint16_t*)p.out + (int64_t)(row0 + r) * p.o_sr + (int64_t)(h * G + g) * p.o_sh + 4 * lq;
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+          uint2 packed;
+          packed.x = (uint32_t)bf16_bits_from_f32(o[k][t][0] * inv) |
+                     ((uint32_t)bf16_bits_from_f32(o[k][t][1] * inv) << 16);
+          packed.y = (uint32_t)bf16_bits_from_f32(o[k][t][2] * inv) |
+                     ((uint32_t)bf16_bits_from_f32(o[k][t][3] * inv) << 16);
+          *(uint2*)(orow + 16 * t) = packed;
+        }
       }
     }
-  }
-}
-
-template <int KT, int D, int G>
-__global__ __launch_bounds__(256) void prefill_stream_kernel(PrefillParams p, const int32_t* __restrict__ tables,
-                                                             const int4* __restrict__ vseq,
-                                                             const int* __restrict__ vtiles,
-                                                             const int* __restrict__ header,
-                                                             const float* __restrict__ kscale,
-                                                             const float* __restrict__ vscale) {
-  constexpr int NC = D / 32;
-  const PIndex ix{tables, vseq, vtiles, kscale, vscale};
-  const int lane = threadIdx.x & 63;
-  const int li = lane & 15, lq = lane >> 4;
-  const int w = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
-  const int Wtot = gridDim.x * 4;
-  const int nv = header[0];
-  const int Tb = header[1];
-  const int64_t T = (int64_t)p.Hkv * Tb;
-  if (T == 0 || nv == 0) return;
-  const int64_t chunk = (T + Wtot - 1) / Wtot;
-  int64_t tau = (int64_t)w * chunk;
-  if (tau >= T) return;
-  const int64_t tau_end = tau + chunk < T ? tau + chunk : T;
-
-  PCoord c0;
-  c0.h = (int)(tau / Tb);
-  {
-    const int r = (int)(tau % Tb);
-    c0.v = find_block(ix, nv, r);
-    c0.j = r - ix.vtiles[c0.v];
-  }
-  set_block(p, ix, c0);
-  fetch_ids(p, ix, c0);
-  bool has1 = tau + 1 < tau_end;
-  PCoord c1 = has1 ? advance(p, ix, c0, nv) : c0;
-
-  const KvCacheView kv{(const uint8_t*)p.k, (const uint8_t*)p.v, p.k_s[0], p.k_s[2], p.v_s[0], p.v_s[2]};
-  TileRegs<KT, D> r0, r1;
-  load_tile<KT, D>(r0, kv, c0.blkA, c0.blkB, li, lq, c0.h);
-  bf16x8_t qop[kNCT][NC];
-  load_q_block<D, G>(qop, p, c0, li, lq);
-  float qk_scale = p.scale * (ix.kscale ? ix.kscale[c0.h * p.ks_s] : 1.0f) * kLog2e;
-  PRun<D> st;
-  st.reset(c0.j);
-  bool first_run = true;
-  for (;;) {
-    load_tile<KT, D>(r1, kv, c1.blkA, c1.blkB, li, lq, c1.h);
-    const bool has2 = has1 && tau + 2 < tau_end;
-    PCoord c2 = has2 ? advance(p, ix, c1, nv) : c1;
-    prefill_tile<KT, D, G>(st, r0, c0, qop, qk_scale, li, lq);
-    const bool run_ends = !has1 || c1.v != c0.v || c1.h != c0.h;
-    if (run_ends) {
-      prefill_flush<D, G>(p, ix, st, c0, tau, chunk, w, first_run, lane);
-      first_run = false;
-    }
-    if (!has1) break;
-    c0 = c1;
-    c1 = c2;
-    has1 = has2;
-    r0 = r1;
-    ++tau;
-    if (run_ends) {
-      load_q_block<D, G>(qop, p, c0, li, lq);
-      qk_scale = p.scale * (ix.kscale ? ix.kscale[c0.h * p.ks_s] : 1.0f) * kLog2e;
-      st.reset(c0.j);
-    }
-  }
-}
-
-// Combines the partials of query blocks split between waves.  One workgroup
-// of 256 threads per (KV head, query block).
-template <int D, int G>
-__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p, const int* __restrict__ header) {
-  constexpr int COLS = 16 * kNCT;
-  constexpr int RPT = 16 / G;
-  const int v = blockIdx.x, h = blockIdx.y;
-  if (v >= header[0]) return;
-  const int2 desc = p.merge_desc[(int64_t)v * p.Hkv + h];
-  const int nslots = desc.y;
-  const int slot_first = desc.x;
-  if (nslots == 0 && slot_first >= 0) return;  // written by the stream kernel
-  const int w1 = slot_first >> 1;
-  const int4 e = p.vseq[v];
-  const int row0 = e.y, rows = e.z;
-  for (int idx = threadIdx.x; idx < COLS * D; idx += blockDim.x) {
-    const int col = idx / D, d = idx % D;
-    const int ct = col / 16, li = col % 16;
-    const int t = ct * RPT + li / G;
-    if (t >= rows) continue;
-    float M = -INFINITY;
-    for (int k = 0; k < nslots; ++k) {
-      const int slot = k == 0 ? slot_first : 2 * (w1 + k);
-      M = fmaxf(M, p.ws_ml[((int64_t)slot * COLS + col) * 2]);
-    }
-    float L = 0.0f, acc = 0.0f;
-    if (M != -INFINITY) {
-      for (int k = 0; k < nslots; ++k) {
-        const int slot = k == 0 ? slot_first : 2 * (w1 + k);
-        const float m = p.ws_ml[((int64_t)slot * COLS + col) * 2];
-        if (m == -INFINITY) continue;
-        const float f = __expf(m - M);
-        L += p.ws_ml[((int64_t)slot * COLS + col) * 2 + 1] * f;
-        acc += p.ws_o[((int64_t)slot * COLS + col) * D + d] * f;
-      }
-    }
-    uint16_t* orow = (uint16_t*)p.out + (int64_t)(row0 + t) * p.o_sr + (int64_t)(h * G + li % G) * p.o_sh;
-    orow[d] = bf16_bits_from_f32(L > 0.0f ? acc / L : 0.0f);
   }
 }
 
@@ -460,29 +457,27 @@ int prefill_cus() {
   return n;
 }
 
-constexpr int kPrefillBlocksPerCU = 1;  // 4-wave workgroups resident per CU
-
-uint64_t pad256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
-uint64_t prefill_waves() { return (uint64_t)prefill_cus() * kPrefillBlocksPerCU * 4; }
+constexpr int kItemBlocksPerCU = 2;  // resident workgroups per CU (8 waves)
 
 template <int KT, int D, int G>
 int32_t launch_t(PrefillParams& p, hipStream_t stream) {
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_item_kernel<KT, D, G>, 256, 0) != hipSuccess ||
+        n < 1)
+      n = 1;
+    per_cu = n < kItemBlocksPerCU ? n : kItemBlocksPerCU;
+  }
   {
     ProfileScope prof("cf_prefill_plan", stream);
-    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(64), 0, stream, p);
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
   }
   CF_HIP_CHECK(hipGetLastError());
-  const int blocks = prefill_cus() * kPrefillBlocksPerCU;
   {
     ProfileScope prof("cf_prefill_mfma", stream);
-    hipLaunchKernelGGL((prefill_stream_kernel<KT, D, G>), dim3(blocks), dim3(256), 0, stream, p, p.tables,
-                       (const int4*)p.vseq, (const int*)p.vtiles, (const int*)p.header, p.k_scale, p.v_scale);
-  }
-  CF_HIP_CHECK(hipGetLastError());
-  {
-    ProfileScope prof("cf_prefill_merge", stream);
-    hipLaunchKernelGGL((prefill_merge_kernel<D, G>), dim3(p.max_v, p.Hkv), dim3(256), 0, stream, p,
-                       (const int*)p.header);
+    hipLaunchKernelGGL((prefill_item_kernel<KT, D, G>), dim3(prefill_cus() * per_cu), dim3(256), 0, stream, p,
+                       p.tables, (const int4*)p.items, (const int4*)p.chunks, p.header, p.k_scale, p.v_scale);
   }
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
@@ -501,6 +496,8 @@ int32_t launch_g(PrefillParams& p, hipStream_t stream) {
   return CF_ERR_UNSUPPORTED;
 }
 
+uint64_t pad256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
+
 }  // namespace
 
 bool prefill_supported(const PrefillParams& p, int q_dt, int kv_dt) {
@@ -518,35 +515,25 @@ bool prefill_supported(const PrefillParams& p, int q_dt, int kv_dt) {
   return true;
 }
 
-// Workspace: [vseq int4 x max_v][vtiles int x (max_v + 1)][header 2 int]
-//            [o: 2 slots per wave x 16*NCT x D f32][(m, l)][merge descs int2 x max_v x Hkv]
+int prefill_rows_per_item(int G) { return kCols / G; }
+
+// Workspace: [chunks int4 x N][items int4 x max_items][header 2 int]
 uint64_t prefill_workspace_bytes(int64_t Tq, int64_t N, int64_t Hq, int64_t Hkv, int64_t D) {
+  (void)D;
   const int64_t G = Hkv > 0 ? Hq / Hkv : 1;
-  const int64_t QB = G > 0 ? kNCT * 16 / G : 1;
-  const uint64_t max_v = (uint64_t)(Tq / QB + N + 1);
-  const uint64_t slots = prefill_waves() * 2;
-  return pad256(max_v * 16) + pad256((max_v + 1) * 4) + 256 + pad256(slots * 16 * kNCT * D * 4) +
-         pad256(slots * 16 * kNCT * 2 * 4) + pad256(max_v * Hkv * 8);
+  const int64_t RB = G > 0 ? kCols / G : 1;
+  const uint64_t max_items = (uint64_t)(Tq / RB + N) * (uint64_t)Hkv;
+  return pad256((uint64_t)N * 16) + pad256(max_items * 16) + 256;
 }
 
 void prefill_bind_workspace(PrefillParams& p, void* workspace) {
-  const uint64_t max_v = (uint64_t)p.max_v;
-  const uint64_t slots = prefill_waves() * 2;
   char* w = (char*)workspace;
-  p.vseq = (int4*)w;
-  w += pad256(max_v * 16);
-  p.vtiles = (int*)w;
-  w += pad256((max_v + 1) * 4);
+  p.chunks = (int4*)w;
+  w += pad256((uint64_t)p.N * 16);
+  p.items = (int4*)w;
+  w += pad256((uint64_t)p.max_items * 16);
   p.header = (int*)w;
-  w += 256;
-  p.ws_o = (float*)w;
-  w += pad256(slots * 16 * kNCT * p.D * 4);
-  p.ws_ml = (float*)w;
-  w += pad256(slots * 16 * kNCT * 2 * 4);
-  p.merge_desc = (int2*)w;
 }
-
-int prefill_query_block(int G) { return kNCT * 16 / G; }
 
 int32_t launch_prefill(PrefillParams& p, int kv_dt, hipStream_t stream) {
   if (kv_dt == kE4M3) {

@@ -26,19 +26,16 @@ struct PrefillParams {
   int64_t ks_s, vs_s;
   float scale;
   int N, Tq, Hq, Hkv, G, D, Mb, NB;
-  int QB;     // query tokens per query block (one virtual sequence)
-  int max_v;  // bound on the number of query blocks: Tq / QB + N + 1
+  int RB;         // query rows per work item (128 / G: 128 query columns)
+  int max_items;  // bound on work items: (Tq / RB + N) * Hkv
   // workspace
-  int4* vseq;         // [max_v] {chunk, first q row, rows, position of the first row}
-  int* vtiles;        // [max_v + 1] tiles before virtual sequence v; [max_v] = total
-  int* header;        // {number of query blocks, tiles per KV head}
-  float* ws_o;        // [2 slots per wave][16 * NCT columns][D]
-  float* ws_ml;       // [2 slots per wave][16 * NCT columns][2]
-  int2* merge_desc;   // [max_v][Hkv]
+  int4* chunks;  // [N] {first q row, rows, position of the first row, row blocks before it}
+  int4* items;   // [max_items] {chunk, row block, KV head, tiles}, longest first
+  int* header;   // {number of items, queue counter}
 };
 
-// Query tokens per query block for GQA group G.
-int prefill_query_block(int G);
+// Query rows per work item for GQA group G.
+int prefill_rows_per_item(int G);
 bool prefill_supported(const PrefillParams& p, int q_dt, int kv_dt);
 uint64_t prefill_workspace_bytes(int64_t Tq, int64_t N, int64_t Hq, int64_t Hkv, int64_t D);
 void prefill_bind_workspace(PrefillParams& p, void* workspace);
