@@ -221,6 +221,131 @@ bool kv_write_native_ok(const KvWriteParams& p, int x_dt) {
   return true;
 }
 
+// ---- row-piece kernels (head_dim a multiple of 16) ------------------------
+// A row is the D elements of one (a, t, h) of a [S0, S1, H, D] view; a piece
+// is 16 consecutive elements of a row.  Pieces load and store as 16-byte
+// vectors where the view's rows are contiguous and 16-byte aligned, element
+// by element otherwise (e.g. the channel-major V layout).
+
+__device__ __forceinline__ int64_t row_offset(const Rank4& v, int64_t a_t, int h) {
+  const int64_t t = a_t % v.size[1], a = a_t / v.size[1];
+  return a * v.stride[0] + t * v.stride[1] + (int64_t)h * v.stride[2];
+}
+
+template <int XT>
+__device__ __forceinline__ void load_piece(const Rank4& x, int64_t off, bool vec, float* f) {
+  using XE = Elem<XT>;
+  const typename XE::T* src = (const typename XE::T*)x.base + off;
+  if (vec) {
+    load16<XT>(src, f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) f[e] = XE::load(src + e * x.stride[3]);
+  }
+}
+
+// One workgroup per (run of rows_per_block rows, head): max |x| over its
+// pieces, one atomic per workgroup.
+template <int XT>
+__global__ __launch_bounds__(256) void amax_rows_kernel(Rank4 x, uint32_t* amax_bits, int rows_per_block, bool vec) {
+  const int h = blockIdx.y;
+  const int64_t rows = x.size[0] * x.size[1];
+  const int np = (int)(x.size[3] / 16);
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t n = (rows - r0 < rows_per_block ? rows - r0 : rows_per_block) * np;
+  uint32_t m = 0;
+  for (int64_t i = threadIdx.x; i < n; i += 256) {
+    const int64_t r = r0 + i / np;
+    const int c = (int)(i % np);
+    float f[16];
+    load_piece<XT>(x, row_offset(x, r, h) + (int64_t)c * 16 * x.stride[3], vec, f);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t u = f2u(f[e]) & 0x7FFFFFFFu;
+      m = m > u ? m : u;
+    }
+  }
+  m = wave_umax(m);
+  __shared__ uint32_t wm[4];
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = wm[0];
+    for (int w = 1; w < 4; ++w) m = m > wm[w] ? m : wm[w];
+    if (m != 0u) atomicMax(amax_bits + h, m);
+  }
+}
+
+// One thread per piece: e4m3fn(x / scales[h]).
+template <int XT>
+__global__ __launch_bounds__(256) void quantize_rows_kernel(Rank4 x, const float* scales, int64_t s_stride, Rank4 out,
+                                                            bool xvec, bool ovec) {
+  const int H = (int)x.size[2];
+  const int np = (int)(x.size[3] / 16);
+  const int64_t n = x.size[0] * x.size[1] * H * np;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int c = (int)(i % np);
+    const int h = (int)((i / np) % H);
+    const int64_t r = i / ((int64_t)np * H);
+    float f[16];
+    load_piece<XT>(x, row_offset(x, r, h) + (int64_t)c * 16 * x.stride[3], xvec, f);
+    const float sc = scales[h * s_stride];
+    uint32_t b[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) b[e] = e4m3_from_f32(f[e] / sc);
+    uint8_t* dst = (uint8_t*)out.base + row_offset(out, r, h) + (int64_t)c * 16 * out.stride[3];
+    if (ovec) {
+      *(uint4*)dst = pack16(b);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dst[e * out.stride[3]] = (uint8_t)b[e];
+    }
+  }
+}
+
+// One thread per piece: f32(code) * scales[h].
+__global__ __launch_bounds__(256) void dequantize_rows_kernel(Rank4 q, const float* scales, int64_t s_stride, Rank4 out,
+                                                              bool qvec, bool ovec) {
+  const int H = (int)q.size[2];
+  const int np = (int)(q.size[3] / 16);
+  const int64_t n = q.size[0] * q.size[1] * H * np;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int c = (int)(i % np);
+    const int h = (int)((i / np) % H);
+    const int64_t r = i / ((int64_t)np * H);
+    const uint8_t* src = (const uint8_t*)q.base + row_offset(q, r, h) + (int64_t)c * 16 * q.stride[3];
+    uint32_t b[16];
+    if (qvec) {
+      const uint4 u = *(const uint4*)src;
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) b[e] = (w[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) b[e] = src[e * q.stride[3]];
+    }
+    const float sc = scales[h * s_stride];
+    float* dst = (float*)out.base + row_offset(out, r, h) + (int64_t)c * 16 * out.stride[3];
+    if (ovec) {
+#pragma unroll
+      for (int e = 0; e < 16; e += 4)
+        *(float4*)(dst + e) = make_float4(f32_from_e4m3(b[e]) * sc, f32_from_e4m3(b[e + 1]) * sc,
+                                          f32_from_e4m3(b[e + 2]) * sc, f32_from_e4m3(b[e + 3]) * sc);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dst[e * out.stride[3]] = f32_from_e4m3(b[e]) * sc;
+    }
+  }
+}
+
+// Whether rows of v (element size eb) load/store as aligned 16-byte pieces.
+bool rows_vectorizable(const Rank4& v, int eb) {
+  if (v.stride[3] != 1 || ((uintptr_t)v.base & 15)) return false;
+  for (int i = 0; i < 3; ++i)
+    if (v.size[i] > 1 && (v.stride[i] * eb) % 16 != 0) return false;
+  return true;
+}
+
 int grid_for(int64_t n) {
   int64_t g = (n + 255) / 256;
   if (g > 65536) g = 65536;
@@ -240,7 +365,20 @@ int32_t launch_amax_scale(const Rank4& x, int x_dt, float* scales, int64_t s_str
   }
   CF_HIP_CHECK(hipGetLastError());
   const int64_t T = x.size[0] * x.size[1];
-  if (T > 0 && x.size[3] > 0) {
+  if (T > 0 && x.size[3] > 0 && x.size[3] % 16 == 0) {
+    // rows of 16-element pieces: ~16 KB per workgroup
+    const int rows = (int)std::max<int64_t>(1, 8192 / x.size[3]);
+    const dim3 grid((unsigned)ceil_div(T, rows), H);
+    const bool vec = rows_vectorizable(x, x_dt == kF32 ? 4 : 2);
+    ProfileScope prof("cf_fp8_amax", stream);
+    switch (x_dt) {
+      case kF32: hipLaunchKernelGGL((amax_rows_kernel<kF32>), grid, dim3(256), 0, stream, x, acc, rows, vec); break;
+      case kF16: hipLaunchKernelGGL((amax_rows_kernel<kF16>), grid, dim3(256), 0, stream, x, acc, rows, vec); break;
+      case kBF16: hipLaunchKernelGGL((amax_rows_kernel<kBF16>), grid, dim3(256), 0, stream, x, acc, rows, vec); break;
+      default: set_error("amax: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
+    }
+    CF_HIP_CHECK(hipGetLastError());
+  } else if (T > 0 && x.size[3] > 0) {
     const int rows = (int)std::max<int64_t>(1, 4096 / std::max<int64_t>(1, x.size[3]));
     const dim3 grid((unsigned)ceil_div(T, rows), H);
     ProfileScope prof("cf_fp8_amax", stream);
@@ -265,6 +403,18 @@ int32_t launch_quantize(const Rank4& x, int x_dt, const float* scales, int64_t s
   const int64_t n = x.size[0] * x.size[1] * x.size[2] * x.size[3];
   if (n == 0) return CF_OK;
   ProfileScope prof("cf_fp8_quantize", stream);
+  if (x.size[3] % 16 == 0) {
+    const dim3 grid(grid_for(n / 16));
+    const bool xv = rows_vectorizable(x, x_dt == kF32 ? 4 : 2), ov = rows_vectorizable(out, 1);
+    switch (x_dt) {
+      case kF32: hipLaunchKernelGGL((quantize_rows_kernel<kF32>), grid, dim3(256), 0, stream, x, scales, s_stride, out, xv, ov); break;
+      case kF16: hipLaunchKernelGGL((quantize_rows_kernel<kF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out, xv, ov); break;
+      case kBF16: hipLaunchKernelGGL((quantize_rows_kernel<kBF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out, xv, ov); break;
+      default: set_error("quantize: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
+    }
+    CF_HIP_CHECK(hipGetLastError());
+    return CF_OK;
+  }
   const dim3 grid(grid_for(n));
   switch (x_dt) {
     case kF32: hipLaunchKernelGGL((quantize_kernel<kF32>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
@@ -281,6 +431,12 @@ int32_t launch_dequantize(const Rank4& q, const float* scales, int64_t s_stride,
   const int64_t n = q.size[0] * q.size[1] * q.size[2] * q.size[3];
   if (n == 0) return CF_OK;
   ProfileScope prof("cf_fp8_dequantize", stream);
+  if (q.size[3] % 16 == 0) {
+    hipLaunchKernelGGL(dequantize_rows_kernel, dim3(grid_for(n / 16)), dim3(256), 0, stream, q, scales, s_stride, out,
+                       rows_vectorizable(q, 1), rows_vectorizable(out, 4));
+    CF_HIP_CHECK(hipGetLastError());
+    return CF_OK;
+  }
   hipLaunchKernelGGL(dequantize_kernel, dim3(grid_for(n)), dim3(256), 0, stream, q, scales, s_stride, out);
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
