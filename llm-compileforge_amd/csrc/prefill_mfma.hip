@@ -306,7 +306,23 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     }
     lmin = uniform(lmin);
     lmax = uniform(lmax);
-    const float qk_scale = p.scale * (kscale ? kscale[h * p.ks_s] : 1.0f) * kLog2e;
+    float qk_scale = p.scale * (kscale ? kscale[h * p.ks_s] : 1.0f) * kLog2e;
+    if (qk_scale < 0.0f) {
+      // the softmax takes its max on raw scores: keep the scale positive by
+      // negating q instead (exact in bf16)
+      qk_scale = -qk_scale;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          uint4 u = __builtin_bit_cast(uint4, qop[k][c]);
+          u.x ^= 0x80008000u;
+          u.y ^= 0x80008000u;
+          u.z ^= 0x80008000u;
+          u.w ^= 0x80008000u;
+          qop[k][c] = as_bf16x8(u);
+        }
+    }
 
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
     f32x4_t o[2][NV];
@@ -335,11 +351,14 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
         const uint4* kl = lds[P];
         const uint4* vl = kl + Gm::KENT;
         bf16x8_t a1[NC], a2[NC];
+        uint4 vraw[NV];
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
           a1[c] = as_bf16x8(kl[c * 64 + lane]);
           a2[c] = as_bf16x8(kl[(NC + c) * 64 + lane]);
         }
+#pragma unroll
+        for (int t = 0; t < NV; ++t) vraw[t] = vl[t * 64 + lane];
         const bool edge = 32 * j + 32 > lmin || !id0.va || !id0.vb;
         const bool blk_ok = lq < 2 ? id0.va : id0.vb;
         const int tok0 = 32 * j + 8 * lq;
@@ -357,8 +376,8 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
           float sc[8];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            sc[v] = s1[v] * qk_scale;
-            sc[4 + v] = s2[v] * qk_scale;
+            sc[v] = s1[v];
+            sc[4 + v] = s2[v];
           }
           if (edge) {
             const int nvalid = blk_ok ? lim[k] - tok0 : 0;
@@ -371,8 +390,9 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
           for (int v = 1; v < 8; ++v) mt = fmaxf(mt, sc[v]);
           mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
           mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+          mt *= qk_scale;  // qk_scale > 0: the max of scaled scores (log2 units)
           // lazy rescale: the running max moves only when a score passes it
-          // by more than 8 (log2 units), so p <= 256
+          // by more than 8, so p <= 256
           if (__any(mt > m[k] + 8.0f)) {
             const float mnew = mt > m[k] + 8.0f ? mt : m[k];
             const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[k] - mnew);
@@ -381,11 +401,13 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
             for (int t = 0; t < NV; ++t) o[k][t] = o[k][t] * alpha;
             m[k] = mnew;
           }
-          const bool live = m[k] != -INFINITY;
+          // a column with nothing visible yet keeps m = -inf; its scores are
+          // all -inf, so any finite reference gives p = 0
+          const float mref = m[k] == -INFINITY ? 0.0f : m[k];
           float psum = 0.0f;
 #pragma unroll
           for (int v = 0; v < 8; ++v) {
-            const float pv = live ? __builtin_amdgcn_exp2f(sc[v] - m[k]) : 0.0f;
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], qk_scale, -mref));
             psum += pv;
             if constexpr (KT == kE4M3) {
               pop[k][v] = (_Float16)pv;
@@ -400,14 +422,13 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
         // ---- O^T += V^T P^T ------------------------------------------------
 #pragma unroll
         for (int t = 0; t < NV; ++t) {
-          const uint4 vraw = vl[t * 64 + lane];
 #pragma unroll
           for (int k = 0; k < 2; ++k) {
             if constexpr (KT == kE4M3) {
-              o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, vraw), pop[k], o[k][t],
+              o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, vraw[t]), pop[k], o[k][t],
                                                                0, 0, 0);
             } else {
-              const bf16x8_t vop = as_bf16x8(vraw);
+              const bf16x8_t vop = as_bf16x8(vraw[t]);
               o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[k], o[k][t], 0, 0, 0);
               o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo[k], o[k][t], 0, 0, 0);
             }
