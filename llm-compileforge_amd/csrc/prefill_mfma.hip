@@ -323,6 +323,11 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
           qop[k][c] = as_bf16x8(u);
         }
     }
+    // A zero scale makes every score 0 (uniform weights over the visible
+    // tokens); the smallest normal scale gives the same weights (products
+    // ~1e-34, exp2 of which is 1.0f) and keeps -inf * scale = -inf for the
+    // masked ones.
+    if (qk_scale == 0.0f) qk_scale = 1.17549435e-38f;
 
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
     f32x4_t o[2][NV];

@@ -229,3 +229,16 @@ def test_invalid_block_ids_contribute_nothing(gpu):
     lens = [case.seq_lens[0] - 16, case.seq_lens[1] - 16, case.seq_lens[2], case.seq_lens[3]]
     ref = oracle_decode(case, kc, vc, ks, vs, tables=[t0, t1, case.block_tables[2], case.block_tables[3]], lens=lens)
     assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, "invalid ids")
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("scale", [-0.09, 0.0, 0.5])
+def test_softmax_scales(gpu, scale, kv_dtype):
+    """Negative, zero (uniform weights) and large softmax scales."""
+    case = workloads.make_case("c3_llama3_8b", device=gpu, seed=17, batch=5)
+    case.kv_dtype = kv_dtype
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    case.scale = scale
+    out = _run(case, kc, vc, ks, vs, gpu)
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, f"decode scale {scale} {kv_dtype}")

@@ -51,7 +51,7 @@ def _remap(tables):
     return used, [[remap[b] for b in t] for t in tables]
 
 
-def oracle_prefill(case, t, q=None, tables=None, lens=None, q_start=None):
+def oracle_prefill(case, t, q=None, tables=None, lens=None, q_start=None, scale=None):
     tables = [list(x) for x in (tables if tables is not None else case.prefill_tables)]
     used, rt = _remap(tables)
     k, v = _cache_values(t["k_cache"], t["v_cache"], used)
@@ -60,13 +60,14 @@ def oracle_prefill(case, t, q=None, tables=None, lens=None, q_start=None):
     q = (q if q is not None else case.q_prefill).float().cpu().numpy()
     return paged_prefill_fp64(q, k, v, rt, list(lens if lens is not None else case.prefill_lens),
                               list(q_start if q_start is not None else case.q_start), case.block_size,
-                              case.scale, ks, vs)
+                              case.scale if scale is None else scale, ks, vs)
 
 
 def _prefill(case, t, **kw):
     out = chunked_prefill_attention(
         kw.get("q", t["q_prefill"]), t["k_cache"], t["v_cache"], kw.get("tables", t["prefill_tables"]),
-        kw.get("lens", t["prefill_lens"]), kw.get("q_start", t["q_start"]), case.block_size, case.scale,
+        kw.get("lens", t["prefill_lens"]), kw.get("q_start", t["q_start"]), case.block_size,
+        kw.get("scale", case.scale),
         k_scale=t["k_scale"], v_scale=t["v_scale"], out=kw.get("out"),
     )
     torch.cuda.synchronize()
@@ -131,6 +132,20 @@ def test_edge_rules(gpu):
     ref2, _ = oracle_prefill(case, t, q=case.q_prefill[:8], tables=case.prefill_tables[:1], lens=[cap + 100],
                              q_start=[0, 8])
     assert_close(out2.float().cpu().numpy(), ref2, torch.bfloat16, "past capacity")
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("scale", [-0.09, 0.0, 0.5])
+def test_softmax_scales(gpu, scale, kv_dtype):
+    """Negative, zero and large softmax scales (the kernel takes its running
+    max on raw scores and negates q for a negative scale)."""
+    case = workloads.make_mixed_case(device=gpu, seed=16, chunks=[40, 70], cached=[30, 200], decode_lens=[],
+                                     kv_dtype=kv_dtype)
+    t = workloads.materialize_mixed(case)
+    _write_new_rows(case, t)
+    out = _prefill(case, t, scale=scale)
+    ref, _ = oracle_prefill(case, t, scale=scale)
+    assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, f"scale {scale}")
 
 
 def test_repeated_calls_shrinking(gpu):
