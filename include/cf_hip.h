@@ -230,6 +230,35 @@ int32_t cf_kv_write_fp8(const CfTensor* k_new, const CfTensor* v_new,
                         CfTensor* v_cache, const CfTensor* k_scale,
                         const CfTensor* v_scale, void* stream);
 
+/* Writes new rows into one paged tensor (a K or a V cache, any layout):
+ * row i goes to block slot_mapping[i] / bs, offset slot_mapping[i] % bs
+ * (reference CacheManager.write_paged placement,
+ * python_runtime/engine/cache_manager.py:139-171; _kv_cache.py:68-104),
+ * converted to the cache dtype (e4m3fn: e4m3fn(f32(x) / scale[h]), the
+ * FP8KVCacheQuantizer arithmetic; bf16/f16: round to nearest even).
+ * Slots < 0 or >= NB * bs are skipped.
+ *   x_new         [T, H, D]        f32 | f16 | bf16
+ *   slot_mapping  [T]              i32 | i64
+ *   cache         [NB, bs, H, D]   f32 | f16 | bf16 | e4m3fn, any strides
+ *   scale         [H] or [1] f32   (e4m3fn caches; NULL otherwise)
+ * The caller must not target a slot that another sequence still reads. */
+int32_t cf_paged_write(const CfTensor* x_new, const CfTensor* slot_mapping,
+                       CfTensor* cache, const CfTensor* scale, void* stream);
+
+/* Gathers the first S tokens of each block table into a dense tensor:
+ * out[r, s] = row s % bs of block block_tables[r][s / bs], dequantized
+ * (e4m3fn: code * scale[h]) and converted to out's dtype; a table entry
+ * outside [0, NB) gives zero rows (pad short tables with -1).  Replaces
+ * CacheManager.read_paged / _gather_kv_flat
+ * (reference python_runtime/engine/cache_manager.py:173-197,
+ * _kv_cache.py:106-132).
+ *   cache         [NB, bs, H, D]   f32 | f16 | bf16 | e4m3fn, any strides
+ *   block_tables  [R, Mb]          i32
+ *   scale         [H] or [1] f32   (e4m3fn caches; NULL otherwise)
+ *   out           [R, S, H, D]     f32 | f16 | bf16, any strides */
+int32_t cf_paged_gather(const CfTensor* cache, const CfTensor* block_tables,
+                        const CfTensor* scale, CfTensor* out, void* stream);
+
 /* Kernel timing hook for benchmarks (no reference counterpart).  While
  * enabled, every kernel this library launches is bracketed by a pair of
  * HIP events recorded on the launch stream.  cf_profile_query synchronizes

@@ -159,6 +159,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "cf_fp8_quantize": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
     "cf_fp8_dequantize": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
     "cf_kv_write_fp8": (ctypes.c_int32, [_P, _P, _P, _P, _P, _P, _P, ctypes.c_void_p]),
+    "cf_paged_write": (ctypes.c_int32, [_P, _P, _P, _P, ctypes.c_void_p]),
+    "cf_paged_gather": (ctypes.c_int32, [_P, _P, _P, _P, ctypes.c_void_p]),
     "cf_profile_enable": (ctypes.c_int32, [ctypes.c_int32]),
     "cf_profile_reset": (ctypes.c_int32, []),
     "cf_profile_query": (

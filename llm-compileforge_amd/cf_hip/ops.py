@@ -339,6 +339,53 @@ def kv_write_fp8(
     check(rc, "cf_kv_write_fp8")
 
 
+def paged_write(
+    x_new: torch.Tensor, slot_mapping: torch.Tensor, cache: torch.Tensor, scale: torch.Tensor | None = None
+) -> None:
+    """Writes rows x_new [T, H, D] into a paged cache [NB, bs, H, D] (any
+    layout) at slots block * bs + offset; e4m3fn caches quantize with the
+    per-head `scale` [H] (or one scale).  Slots outside the cache are skipped."""
+    for name, t in (("x_new", x_new), ("slot_mapping", slot_mapping), ("cache", cache)):
+        _require_device(name, t)
+    dev = _same_device(x_new, slot_mapping, cache)
+    ds = [descriptor(t) for t in (x_new, slot_mapping, cache)]
+    dsc = None
+    if scale is not None:
+        _require_device("scale", scale)
+        dsc = descriptor(scale.reshape(-1))
+    with torch.cuda.device(dev):
+        rc = lib().cf_paged_write(ref(ds[0]), ref(ds[1]), ref(ds[2]), ref(dsc), stream_handle(dev))
+    check(rc, "cf_paged_write")
+
+
+def paged_gather(
+    cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_len: int,
+    out_dtype: torch.dtype | None = None,
+    scale: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Dense [R, seq_len, H, D] rows of the tables' first seq_len tokens
+    (e4m3fn caches dequantized with `scale`, returned as float32 unless
+    out_dtype says otherwise); table entries < 0 give zero rows."""
+    _require_device("cache", cache)
+    _require_device("block_tables", block_tables)
+    dev = _same_device(cache, block_tables)
+    if out is None:
+        dt = out_dtype or (torch.float32 if cache.dtype == torch.float8_e4m3fn else cache.dtype)
+        out = torch.empty(block_tables.shape[0], seq_len, cache.shape[2], cache.shape[3], dtype=dt, device=dev)
+    dsc = None
+    if scale is not None:
+        _require_device("scale", scale)
+        dsc = descriptor(scale.reshape(-1))
+    dc, dt_, do = descriptor(cache), descriptor(block_tables), descriptor(out)
+    with torch.cuda.device(dev):
+        rc = lib().cf_paged_gather(ref(dc), ref(dt_), ref(dsc), ref(do), stream_handle(dev))
+    check(rc, "cf_paged_gather")
+    return out
+
+
 class KernelTimer:
     """Sums device time of this library's kernel launches (HIP events)."""
 
@@ -375,6 +422,8 @@ __all__ = [
     "fp8_quantize",
     "kv_write_fp8",
     "paged_decode",
+    "paged_gather",
+    "paged_write",
     "shared_prefix_lens",
     "_abi",
 ]

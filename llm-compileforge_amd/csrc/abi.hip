@@ -13,6 +13,7 @@
 #include "cf_host.hpp"
 #include "decode_params.hpp"
 #include "kv_fp8.hpp"
+#include "paged_io.hpp"
 #include "prefill_params.hpp"
 
 namespace cf {
@@ -537,6 +538,89 @@ int32_t cf_kv_write_fp8(const CfTensor* k_new, const CfTensor* v_new, const CfTe
   p.bs = (int)vkc.size[1];
   p.NB = vkc.size[0];
   return launch_kv_write_fp8(p, vk.dtype, vsl.dtype, as_stream(stream));
+}
+
+int32_t cf_paged_write(const CfTensor* x_new, const CfTensor* slot_mapping, CfTensor* cache, const CfTensor* scale,
+                       void* stream) {
+  View vx, vsl, vc;
+  int32_t rc;
+  if ((rc = view_of(x_new, "x_new", 3, &vx))) return rc;
+  if ((rc = view_of(slot_mapping, "slot_mapping", 1, &vsl))) return rc;
+  if ((rc = view_of(cache, "cache", 4, &vc))) return rc;
+  CF_CHECK(is_float_dtype(vx.dtype), "x_new: dtype must be f32, f16 or bf16, got %s", dtype_name(vx.dtype));
+  CF_CHECK(vsl.dtype == CF_I32 || vsl.dtype == CF_I64, "slot_mapping: expected i32 or i64, got %s",
+           dtype_name(vsl.dtype));
+  CF_CHECK(is_float_dtype(vc.dtype) || vc.dtype == CF_F8E4M3FN,
+           "cache: dtype must be f32, f16, bf16 or f8e4m3fn, got %s", dtype_name(vc.dtype));
+  const int64_t T = vx.size[0], H = vx.size[1], D = vx.size[2];
+  CF_CHECK(vsl.size[0] == T, "slot_mapping has %lld entries, %lld rows given", (long long)vsl.size[0], (long long)T);
+  CF_CHECK(vc.size[2] == H && vc.size[3] == D, "cache [NB, bs, %lld, %lld] does not match rows [T, %lld, %lld]",
+           (long long)vc.size[2], (long long)vc.size[3], (long long)H, (long long)D);
+  CF_CHECK(vc.size[1] > 0, "cache block size must be positive");
+  CF_CHECK(H < 65536 && D < 65536 && vc.size[1] < 65536, "cache dims too large");
+  PagedWriteParams p{};
+  if (vc.dtype == CF_F8E4M3FN) {
+    CF_CHECK(scale != nullptr, "f8e4m3fn caches need a scale");
+    if ((rc = scale_view(scale, "scale", H, &p.scale, &p.sc_s))) return rc;
+  } else {
+    CF_CHECK(scale == nullptr, "scale applies to f8e4m3fn caches only");
+  }
+  p.x = vx.base;
+  for (int i = 0; i < 3; ++i) p.x_s[i] = vx.stride[i];
+  p.slots = vsl.base;
+  p.slot_s = vsl.stride[0];
+  p.cache = vc.base;
+  for (int i = 0; i < 4; ++i) p.c_s[i] = vc.stride[i];
+  p.T = T;
+  p.NB = vc.size[0];
+  p.H = (int)H;
+  p.D = (int)D;
+  p.bs = (int)vc.size[1];
+  return launch_paged_write(p, vx.dtype, vsl.dtype, vc.dtype, as_stream(stream));
+}
+
+int32_t cf_paged_gather(const CfTensor* cache, const CfTensor* block_tables, const CfTensor* scale, CfTensor* out,
+                        void* stream) {
+  View vc, vt, vo;
+  int32_t rc;
+  if ((rc = view_of(cache, "cache", 4, &vc))) return rc;
+  if ((rc = view_of(block_tables, "block_tables", 2, &vt))) return rc;
+  if ((rc = view_of(out, "out", 4, &vo))) return rc;
+  CF_CHECK(is_float_dtype(vc.dtype) || vc.dtype == CF_F8E4M3FN,
+           "cache: dtype must be f32, f16, bf16 or f8e4m3fn, got %s", dtype_name(vc.dtype));
+  CF_CHECK(vt.dtype == CF_I32, "block_tables: expected i32, got %s", dtype_name(vt.dtype));
+  CF_CHECK(is_float_dtype(vo.dtype), "out: dtype must be f32, f16 or bf16, got %s", dtype_name(vo.dtype));
+  const int64_t R = vt.size[0];
+  CF_CHECK(vo.size[0] == R && vo.size[2] == vc.size[2] && vo.size[3] == vc.size[3],
+           "out must be [%lld, S, %lld, %lld]", (long long)R, (long long)vc.size[2], (long long)vc.size[3]);
+  CF_CHECK(vc.size[1] > 0, "cache block size must be positive");
+  CF_CHECK(R < (int64_t)INT32_MAX && vo.size[1] < (int64_t)INT32_MAX && vt.size[1] < (int64_t)INT32_MAX &&
+               vc.size[2] < 65536 && vc.size[3] < 65536 && vc.size[1] < 65536,
+           "gather dims too large");
+  PagedGatherParams p{};
+  if (vc.dtype == CF_F8E4M3FN) {
+    CF_CHECK(scale != nullptr, "f8e4m3fn caches need a scale");
+    if ((rc = scale_view(scale, "scale", vc.size[2], &p.scale, &p.sc_s))) return rc;
+  } else {
+    CF_CHECK(scale == nullptr, "scale applies to f8e4m3fn caches only");
+  }
+  p.cache = vc.base;
+  for (int i = 0; i < 4; ++i) {
+    p.c_s[i] = vc.stride[i];
+    p.o_s[i] = vo.stride[i];
+  }
+  p.tables = (const int32_t*)vt.base;
+  p.t_sr = vt.stride[0];
+  p.t_sm = vt.stride[1];
+  p.out = vo.base;
+  p.NB = vc.size[0];
+  p.R = (int)R;
+  p.Mb = (int)vt.size[1];
+  p.S = (int)vo.size[1];
+  p.H = (int)vc.size[2];
+  p.D = (int)vc.size[3];
+  p.bs = (int)vc.size[1];
+  return launch_paged_gather(p, vc.dtype, vo.dtype, as_stream(stream));
 }
 
 int32_t cf_profile_enable(int32_t on) {
