@@ -2,9 +2,10 @@
 
 Drop-in for the reference's CacheManager
 (python_runtime/engine/cache_manager.py:79-267): same constructor, policy
-formats (a proto-like SfaCachePolicy object or the JSON dict of metadata.json,
-converted by `_dict_to_proto_cache_policy`, :30-66), slab shapes, per-step
-state and read/write semantics.  What differs is where the bytes live and
+formats (an SfaCachePolicy message or the JSON dict of metadata.json,
+converted by `_dict_to_proto_cache_policy`, :30-66; also the serialized
+blob and compiler.cache_policy.CachePolicy), slab shapes, per-step state
+and read/write semantics.  What differs is where the bytes live and
 what moves them:
 
 - Slabs live in HBM (the device given, default the current GPU).  A paged
@@ -22,8 +23,8 @@ what moves them:
 - read_paged gathers the requests' blocks, in sorted request-id order with
   zeros past each table (:173-197), in one launch (cf_paged_gather).
 - Slabs may be "float8_e4m3fn": rows are quantized on write with per-(layer,
-  head) scales and dequantized on read (float32 result); attention reads the
-  codes directly.
+  head) scales (from the policy, else 1.0, settable) and dequantized on read
+  (float32 result); attention reads the codes directly.
 - attend() (no reference counterpart) runs decode attention for one query
   row per request straight from the slabs.
 
@@ -35,92 +36,68 @@ from __future__ import annotations
 
 import logging
 import math
-from dataclasses import dataclass, field
 from typing import Any
 
 import numpy as np
 import torch
 
 from cf_hip import ops as _ops
+from compiler.sfa_cache_proto import SfaCachePolicy, SfaInterceptSpec, SfaSlabSpec
 
 _logger = logging.getLogger(__name__)
 
 _ROLE_KEY, _ROLE_VALUE, _ROLE_PLAIN = "k", "v", "plain"
 
 
-# ── Policy (proto-like) ───────────────────────────────────────────────
-
-
-@dataclass
-class SfaSlabSpec:
-    """Field-for-field stand-in of the SfaSlabSpec proto message
-    (reference proto/sfa_abi.proto, used at cache_manager.py:43-51)."""
-
-    name: str = ""
-    slab_type: str = ""
-    layout: str = ""
-    dtype: str = "float32"
-    block_size: int = 16
-    num_layers: int = 0
-    num_heads: int = 0
-    head_dim: int = 0
-
-
-@dataclass
-class SfaInterceptSpec:
-    """Stand-in of the SfaInterceptSpec proto message (cache_manager.py:52-65)."""
-
-    slab_id: str = ""
-    op_name_pattern: str = ""
-    intercept_type: str = ""
-    source: str = ""
-    layer: str = "sequential"
-    param_indices: list[int] = field(default_factory=list)
-
-
-@dataclass
-class SfaCachePolicy:
-    """Stand-in of the SfaCachePolicy proto message.  CacheManager reads only
-    the attributes (block_size, max_requests, slabs, intercepts), so a real
-    proto object works the same."""
-
-    block_size: int = 16
-    max_requests: int = 256
-    slabs: list[SfaSlabSpec] = field(default_factory=list)
-    intercepts: list[SfaInterceptSpec] = field(default_factory=list)
+# ── Policy ────────────────────────────────────────────────────────────
 
 
 def _dict_to_proto_cache_policy(raw: dict[str, Any]) -> SfaCachePolicy:
-    """JSON cache_policy dict (metadata.json) -> policy object, with the
-    reference's field mapping and defaults (cache_manager.py:30-66)."""
+    """JSON cache_policy dict (metadata.json) -> SfaCachePolicy message, with
+    the reference's field mapping and defaults (cache_manager.py:30-66);
+    an FP8 slab's "scales" [layers][heads] go to SlabSpec.scales."""
     block_size = int(raw.get("block_size", 16))
-    policy = SfaCachePolicy(block_size=block_size, max_requests=int(raw.get("max_requests", 256)))
+    policy = SfaCachePolicy()
+    policy.block_size = block_size
+    policy.max_requests = int(raw.get("max_requests", 256))
     for s in raw.get("slabs", []):
         dims = s["dims"]
-        policy.slabs.append(
-            SfaSlabSpec(
-                name=s["slab_id"],
-                slab_type=s["storage"],
-                layout=s.get("layout", ""),
-                dtype=s.get("dtype", "float32"),
-                block_size=block_size,
-                num_layers=int(dims.get("layers", 0)),
-                num_heads=int(dims.get("heads", 0)),
-                head_dim=int(dims.get("dim", 0)),
-            )
-        )
+        slab = policy.slabs.add()
+        slab.name = s["slab_id"]
+        slab.slab_type = s["storage"]
+        slab.layout = s.get("layout", "")
+        slab.dtype = s.get("dtype", "float32")
+        slab.block_size = block_size
+        slab.num_layers = int(dims.get("layers", 0))
+        slab.num_heads = int(dims.get("heads", 0))
+        slab.head_dim = int(dims.get("dim", 0))
+        if s.get("scales") is not None:
+            slab.scales.extend(float(x) for row in s["scales"] for x in row)
     for i in raw.get("intercepts", []):
-        spec = SfaInterceptSpec(
-            slab_id=i["slab_id"],
-            op_name_pattern=i["op_name"],
-            intercept_type=i["direction"],
-            source=i.get("source", ""),
-            layer=i.get("layer", "sequential"),
-        )
+        spec = policy.intercepts.add()
+        spec.slab_id = i["slab_id"]
+        spec.op_name_pattern = i["op_name"]
+        spec.intercept_type = i["direction"]
+        spec.source = i.get("source", "")
+        spec.layer = i.get("layer", "sequential")
         for key in ("func_index", "output_index"):
             if i.get(key) is not None:
                 spec.param_indices.append(int(i[key]))
-        policy.intercepts.append(spec)
+    return policy
+
+
+def _as_policy(policy: Any) -> Any:
+    """Accepted policy forms: an SfaCachePolicy message (this package's or
+    protoc-generated), its serialized bytes, the metadata.json dict, or a
+    compiler.cache_policy.CachePolicy."""
+    if isinstance(policy, (bytes, bytearray, memoryview)):
+        msg = SfaCachePolicy()
+        msg.ParseFromString(bytes(policy))
+        return msg
+    if isinstance(policy, dict):
+        return _dict_to_proto_cache_policy(policy)
+    if hasattr(policy, "to_dict") and not hasattr(policy, "SerializeToString"):
+        return _dict_to_proto_cache_policy(policy.to_dict())
     return policy
 
 
@@ -270,14 +247,15 @@ class CacheManager:
     """Manages cache slabs and positional I/O at runtime (device-resident).
 
     Args:
-        policy: SfaCachePolicy (proto or the stand-in above) or its JSON dict.
+        policy: SfaCachePolicy message, its serialized bytes, the
+            metadata.json dict or a compiler.cache_policy.CachePolicy;
+            FP8 slabs take their scales from it (1.0 where absent).
         num_blocks: physical blocks per paged slab.
         device: where the slabs live (default: the current GPU).
     """
 
     def __init__(self, policy: Any, num_blocks: int, device: torch.device | str | None = None) -> None:
-        if isinstance(policy, dict):
-            policy = _dict_to_proto_cache_policy(policy)
+        policy = _as_policy(policy)
         if device is None:
             if not torch.cuda.is_available():
                 raise RuntimeError("CacheManager needs a GPU (no device given and none is visible)")
@@ -305,9 +283,17 @@ class CacheManager:
             self._slabs[spec.name] = self._allocate_slab(spec)
             self._layer_counters[spec.name] = 0
             if self._slabs[spec.name].dtype == torch.float8_e4m3fn:
-                self._scales[spec.name] = torch.ones(
-                    max(spec.num_layers, 1), max(spec.num_heads, 1), dtype=torch.float32, device=self._device
-                )
+                shape = (max(spec.num_layers, 1), max(spec.num_heads, 1))
+                stored = list(getattr(spec, "scales", []))
+                if stored:
+                    if len(stored) != shape[0] * shape[1]:
+                        raise ValueError(f"slab {spec.name!r}: {len(stored)} scales for {shape[0]} x {shape[1]}")
+                    sc = torch.tensor(stored, dtype=torch.float32).reshape(shape)
+                    if not bool(torch.all(torch.isfinite(sc) & (sc > 0))):
+                        raise ValueError(f"slab {spec.name!r}: FP8 scales must be finite and positive")
+                else:
+                    sc = torch.ones(shape, dtype=torch.float32)
+                self._scales[spec.name] = sc.to(self._device)
 
     def _allocate_slab(self, spec: Any) -> torch.Tensor:
         dtype = _dtype_from_str(spec.dtype)

@@ -21,6 +21,16 @@ Ops:
                       k_scale, v_scale.  Returns [Tq, Hq, D].
   kv_cache_write_fp8  inputs [k_new, v_new, slot_mapping, key_cache,
                       value_cache, k_scale, v_scale]; returns key_cache.
+  cache_write         the planned hal.cache_write (HALOps.td:195-199):
+                      inputs [key, value, slot_mapping, key_cache,
+                      value_cache]; caches of any float dtype and layout,
+                      e4m3fn caches quantize with kwargs k_scale / v_scale;
+                      slots outside the cache are skipped.  Returns key_cache.
+  cache_read          the planned hal.cache_read (HALOps.td:190-194):
+                      inputs [key_cache, value_cache, block_table]; kwargs
+                      seq_len (default: the whole table), k_scale, v_scale,
+                      out_dtype.  Returns [2, R, seq_len, Hkv, D] (keys,
+                      values); ids outside the cache read as zeros.
   fp8_amax_scale      inputs [x]; per-head scales [H] (head axis -2).
   fp8_quantize        inputs [x, scales]; e4m3fn codes.
   fp8_dequantize      inputs [codes, scales]; float32 values.
@@ -42,6 +52,8 @@ _ARITY: dict[str, tuple[int, int]] = {
     "paged_attention": (4, 5),
     "chunked_prefill_attention": (6, 6),
     "kv_cache_write_fp8": (7, 7),
+    "cache_write": (5, 5),
+    "cache_read": (3, 3),
     "fp8_amax_scale": (1, 1),
     "fp8_quantize": (2, 2),
     "fp8_dequantize": (2, 2),
@@ -63,6 +75,8 @@ class HipBackend(OpExecutor):
             "paged_attention": self._paged_attention,
             "chunked_prefill_attention": self._chunked_prefill,
             "kv_cache_write_fp8": self._kv_cache_write_fp8,
+            "cache_write": self._cache_write,
+            "cache_read": self._cache_read,
             "fp8_amax_scale": lambda inputs, **kw: _ops.fp8_amax_scale(inputs[0]),
             "fp8_quantize": lambda inputs, **kw: _ops.fp8_quantize(inputs[0], inputs[1]),
             "fp8_dequantize": lambda inputs, **kw: _ops.fp8_dequantize(inputs[0], inputs[1]),
@@ -118,6 +132,23 @@ class HipBackend(OpExecutor):
         k_new, v_new, slots, k_cache, v_cache, k_scale, v_scale = inputs
         _ops.kv_write_fp8(k_new, v_new, slots, k_cache, v_cache, k_scale, v_scale)
         return k_cache
+
+
+    def _cache_write(self, inputs: list[Any], **kw: Any) -> torch.Tensor:
+        key, value, slots, k_cache, v_cache = inputs
+        _ops.paged_write(key, slots, k_cache, kw.get("k_scale"))
+        _ops.paged_write(value, slots, v_cache, kw.get("v_scale"))
+        return k_cache
+
+    def _cache_read(self, inputs: list[Any], **kw: Any) -> torch.Tensor:
+        k_cache, v_cache, table = inputs
+        seq_len = int(kw.get("seq_len", table.shape[1] * k_cache.shape[1]))
+        dt = kw.get("out_dtype") or (torch.float32 if k_cache.dtype == torch.float8_e4m3fn else k_cache.dtype)
+        out = torch.empty(2, table.shape[0], seq_len, k_cache.shape[2], k_cache.shape[3], dtype=dt,
+                          device=k_cache.device)
+        _ops.paged_gather(k_cache, table, seq_len, scale=kw.get("k_scale"), out=out[0])
+        _ops.paged_gather(v_cache, table, seq_len, scale=kw.get("v_scale"), out=out[1])
+        return out
 
 
 def register_hip_backend(name: str = "hip") -> None:

@@ -208,7 +208,7 @@ def test_policy_from_dict():
     assert pol.block_size == 16 and pol.max_requests == 256
     assert [s.name for s in pol.slabs] == ["k", "v"]
     assert pol.slabs[0].num_layers == 4 and pol.slabs[0].num_heads == 8 and pol.slabs[0].head_dim == 64
-    assert pol.intercepts[0].param_indices == [3, 1] and pol.intercepts[1].param_indices == []
+    assert list(pol.intercepts[0].param_indices) == [3, 1] and list(pol.intercepts[1].param_indices) == []
     assert pol.intercepts[1].source == "operand[2]"
 
 

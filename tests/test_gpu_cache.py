@@ -312,3 +312,62 @@ def test_cache_manager_attend(gpu, dtype):
         want_full = paged_attention_fp64(q.float().numpy(), kf, vf, tables, [len(t) * 16 for t in tables], 16,
                                          scale, ks, vs)
         assert_close(full.float().cpu().numpy(), want_full, torch.bfloat16, f"attend {dtype} full {layer}")
+
+
+def test_cache_manager_from_fp8_policy_blob(gpu):
+    """An FP8 policy blob with stored scales drives the writes: slab codes and
+    reads equal the oracle's with those scales."""
+    from compiler.cache_policy import CachePolicy, serialize_cache_policy
+
+    policy = CachePolicy.for_llama(2, 4, 32, kv_dtype="float8_e4m3fn")
+    gen = torch.Generator().manual_seed(21)
+    sc = {n: (torch.rand(2, 4, generator=gen) * 0.1 + 0.01) for n in ("k", "v")}
+    for n in ("k", "v"):
+        policy.set_kv_scales(n, sc[n])
+    mgr = CacheManager(serialize_cache_policy(policy), num_blocks=6, device=gpu)
+    bt = {"b": [5, 0], "a": [3]}
+    mgr.begin_step(bt)
+    ref = {n: np.zeros((6, 2, 16, 4, 32), np.uint8) for n in ("k", "v")}
+    for layer in range(2):
+        for n in ("k", "v"):
+            x = torch.randn(32, 4, 32, generator=gen).to(torch.bfloat16)
+            mgr.write_paged(n, layer, x, torch.arange(32))
+            s32 = mgr.kv_scales(n)[layer].cpu().numpy()
+            ocm.write_paged(ref[n], layer, x.double().numpy(), list(range(32)), bt, scale=s32)
+    torch.cuda.synchronize()
+    for n in ("k", "v"):
+        np.testing.assert_array_equal(_oracle_slab(mgr, n), ref[n])
+        for layer in range(2):
+            s32 = mgr.kv_scales(n)[layer].cpu().numpy()
+            np.testing.assert_array_equal(s32, sc[n][layer].numpy().astype(np.float32))
+            got = mgr.read_paged(n, layer, 40).double().cpu().numpy()
+            np.testing.assert_array_equal(got, ocm.read_paged(ref[n], layer, 40, bt, scale=s32))
+
+
+def test_hal_cache_ops(gpu):
+    """HipBackend cache_write / cache_read equal the row I/O entry points."""
+    from python_runtime.hal.hip_backend import HipBackend
+    from cf_hip.layout import alloc_kv_cache
+
+    gen = torch.Generator().manual_seed(13)
+    be = HipBackend()
+    kc, vc = alloc_kv_cache(6, 16, 2, 64, E4M3, gpu, "native")
+    kc2, vc2 = alloc_kv_cache(6, 16, 2, 64, E4M3, gpu, "native")
+    for c in (kc, vc, kc2, vc2):  # unwritten slots must agree too
+        c.view(torch.uint8).zero_()
+    ks = (torch.rand(2, generator=gen) + 0.1).to(gpu)
+    vs = (torch.rand(2, generator=gen) + 0.1).to(gpu)
+    k = torch.randn(20, 2, 64, generator=gen).to(torch.bfloat16).to(gpu)
+    v = torch.randn(20, 2, 64, generator=gen).to(torch.bfloat16).to(gpu)
+    slots = torch.randperm(96, generator=gen)[:20].to(gpu)
+    assert be.execute("cache_write", [k, v, slots, kc, vc], k_scale=ks, v_scale=vs) is kc
+    ops.paged_write(k, slots, kc2, ks)
+    ops.paged_write(v, slots, vc2, vs)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(codes(kc), codes(kc2))
+    np.testing.assert_array_equal(codes(vc), codes(vc2))
+    table = torch.tensor([[3, 1], [5, -1]], dtype=torch.int32, device=gpu)
+    out = be.execute("cache_read", [kc, vc, table], k_scale=ks, v_scale=vs, seq_len=20)
+    assert out.shape == (2, 2, 20, 2, 64) and out.dtype == torch.float32
+    assert torch.equal(out[0], ops.paged_gather(kc, table, 20, scale=ks))
+    assert torch.equal(out[1], ops.paged_gather(vc, table, 20, scale=vs))

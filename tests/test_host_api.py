@@ -87,6 +87,12 @@ def test_hip_backend_dispatch_and_errors():
     with pytest.raises(NotImplementedError):
         be.send_kv_cache(None, "x")
     assert "paged_attention" in HipBackend.supported_ops()
+    assert {"cache_read", "cache_write"} <= set(HipBackend.supported_ops())
+    with pytest.raises(ValueError, match="at least 5"):
+        be.execute("cache_write", [torch.zeros(1)] * 4)
+    with pytest.raises(ValueError, match="ROCm device"):
+        be.execute("cache_read", [torch.zeros(2, 16, 1, 8), torch.zeros(2, 16, 1, 8),
+                                  torch.zeros(1, 1, dtype=torch.int32)])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
