@@ -12,6 +12,10 @@ Prints one JSON line (rank 0).  The CPU baseline is the oracle's
 restatement of the reference CPU path (gather + dequantize + SDPA) on a
 bounded sample of the same workload, timed on this host's cores.
 
+`--config block_tables` times per-step block-table upkeep for 256 decoding
+requests (full rebuild + upload vs the block pool's device deltas) and
+copy-on-write block copies over Llama-3-8B-shaped FP8 slabs.
+
 `--config c5_mixed` times BASELINE.json configs[4] instead: one mixed
 step = FP8 write of the step's 4344 new K/V rows + decode attention of 248
 sequences + chunked-prefill attention of 8 x 512-token chunks, all on one
@@ -171,6 +175,137 @@ def bench_mixed(args) -> dict:
     }
 
 
+def bench_block_tables(args) -> dict:
+    """Per-step block-table upkeep for B decoding requests (default 256):
+    rebuilding and uploading the [B, Mb] tables every step, as a dict-based
+    caller does, against the block pool's incremental device tables; plus
+    copy-on-write block copies over Llama-3-8B-shaped FP8 slabs."""
+    import random
+
+    import numpy as np
+    import torch
+
+    from cf_hip import ops
+    from compiler.cache_policy import CachePolicy
+    from python_runtime.engine import CacheManager
+    from python_runtime.engine.block_manager import BlockManager, RequestBatch
+
+    dev = torch.device("cuda:0")
+    B = args.batch or 256
+    bs = 16
+    rng = random.Random(0)
+    lens = [rng.randint(1024, 8192) for _ in range(B)]
+    grow = 2 * (args.steps + args.warmup) + 20 + bs  # tokens appended over both timed paths and the scatter timing
+    cols = -(-(max(lens) + grow) // bs)
+    nb = sum(-(-(n + grow) // bs) for n in lens) + 64
+    bm = BlockManager(nb, bs)
+    ids = [f"req{i}" for i in range(B)]
+    # half the requests share a 1024-token prefix, as a radix hit gives them
+    bm.allocate(ids[0], lens[0])
+    for i in range(1, B):
+        if i < B // 2:
+            bm.share_prefix(ids[0], ids[i], 1024)
+            bm.ensure_blocks(ids[i], lens[i])
+        else:
+            bm.allocate(ids[i], lens[i])
+    for rid, n in zip(ids, lens):
+        bm.set_len(rid, n)
+    bm.bind_device(B, cols, dev)
+    bm.sync_device()
+    host_tables = {rid: bm.get_blocks(rid) for rid in ids}
+    batch = RequestBatch(ids)
+    cur = np.asarray(lens, dtype=np.int64)
+    one = np.ones(B, dtype=np.int64)
+
+    def step_rebuild():
+        # a dict-based caller: host tables -> padded int32 [B, Mb] + lengths, uploaded whole
+        slots, _ = bm.prepare_writes_batch(batch, cur, one)
+        cur[:] += 1
+        for i in np.nonzero((cur - 1) % bs == 0)[0]:
+            host_tables[ids[i]] = bm.get_blocks(ids[i])
+        mat = np.full((B, cols), -1, np.int32)
+        for i, rid in enumerate(ids):
+            t = host_tables[rid]
+            mat[i, : len(t)] = t
+        tables = torch.from_numpy(mat).to(dev)
+        lens_t = torch.from_numpy(cur.astype(np.int32)).to(dev)
+        slots_t = torch.from_numpy(slots).to(dev)
+        return tables, lens_t, slots_t
+
+    def step_deltas():
+        # the block pool: only the changed cells and lengths go to the device
+        slots, _ = bm.prepare_writes_batch(batch, cur, one)
+        cur[:] += 1
+        tables, lens_t = bm.sync_device()
+        return tables, lens_t, torch.from_numpy(slots).to(dev, non_blocking=True)
+
+    res = {}
+    for name, fn in (("rebuild", step_rebuild), ("deltas", step_deltas)):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        res[name] = (time.perf_counter() - t0) * 1e6 / args.steps
+    t, l_ = bm.sync_device()
+    tcpu, lcpu = t.cpu().numpy(), l_.cpu().numpy()
+    for i, rid in enumerate(ids):
+        r = bm.row_of(rid)
+        blocks = bm.get_blocks(rid)
+        assert lcpu[r] == cur[i] and (tcpu[r, : len(blocks)] == blocks).all() and (tcpu[r, len(blocks):] == -1).all(), \
+            "device tables diverged"
+    log(f"B={B}: rebuild {res['rebuild']:.1f} us/step, deltas {res['deltas']:.1f} us/step")
+
+    # copy-on-write copies over Llama-3-8B-shaped FP8 slabs (32 layers, 8 KV heads, D 128)
+    mgr = CacheManager(CachePolicy.for_llama(32, 8, 128, kv_dtype="float8_e4m3fn"), num_blocks=2048, device=dev)
+    pairs = np.stack([np.arange(0, 512), np.arange(1024, 1536)], axis=1).astype(np.int32)
+    block_bytes = sum(s[0].numel() * s.element_size() for s in mgr.paged_slabs())  # K + V of one block
+    for _ in range(3):
+        BlockManager.copy_blocks(pairs, mgr.paged_slabs())
+    torch.cuda.synchronize()
+    with ops.KernelTimer() as timer:
+        for _ in range(10):
+            BlockManager.copy_blocks(pairs, mgr.paged_slabs())
+        torch.cuda.synchronize()
+    ms, n = timer.query("cf_copy_blocks")
+    apply_ms, apply_n = 0.0, 0
+    with ops.KernelTimer() as timer2:
+        for _ in range(20):
+            step_deltas()
+        torch.cuda.synchronize()
+    apply_ms, apply_n = timer2.query("cf_block_tables_apply")
+    copy_s = ms / 10 / 1e3  # one copy_blocks call = K and V slabs
+    moved = 2 * len(pairs) * block_bytes  # read + write
+    gbs = moved / copy_s / 1e9
+    log(f"COW copy of {len(pairs)} blocks ({block_bytes / 2**20:.2f} MiB each, K+V, 32 layers): "
+        f"{copy_s * 1e6:.1f} us, {gbs:.0f} GB/s; table scatter {apply_ms / max(apply_n, 1) * 1e3:.1f} us")
+    return {
+        "metric": "block-table upkeep per decode step (host + upload), B requests, 1 MI355X",
+        "value": res["deltas"],
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["deltas"] / 1e3,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32 tables",
+        "data": "synthetic (seeded)",
+        "config": {"workload": "block_tables", "requests": B, "block_size": bs, "ctx": "U{1024..8192}",
+                   "shared_prefix": "requests 0..B/2-1 share 1024 tokens", "table_cols": cols,
+                   "parallelism": "single GPU"},
+        "rebuild_us_per_step": res["rebuild"],
+        "deltas_us_per_step": res["deltas"],
+        "table_scatter_us": apply_ms / max(apply_n, 1) * 1e3,
+        "roofline": {"bound": "hbm", "kernel": "cf_copy_blocks", "achieved": gbs, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "work": f"{len(pairs)} block copies of {block_bytes} B (read + write)"},
+    }
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,6 +336,10 @@ def main() -> None:
     log(f"device {torch.cuda.get_device_name(dev)}; building {args.config}")
     if args.config == "c5_mixed":
         result = bench_mixed(args)
+        print(json.dumps(result), flush=True)
+        return
+    if args.config == "block_tables":
+        result = bench_block_tables(args)
         print(json.dumps(result), flush=True)
         return
     case = workloads.make_case(args.config, device=dev, seed=0, batch=args.batch)

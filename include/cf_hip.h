@@ -57,6 +57,8 @@ enum {
     CF_ERR_HIP = -2,         /* a HIP runtime call failed                  */
     CF_ERR_WORKSPACE = -3,   /* workspace missing or too small             */
     CF_ERR_UNSUPPORTED = -4, /* valid request this build does not handle   */
+    CF_ERR_OUT_OF_BLOCKS = -5, /* block pool exhausted                     */
+    CF_ERR_NOT_FOUND = -6,   /* unknown request id                         */
 };
 
 /* ABI version of the loaded library (compare with CF_ABI_VERSION).
@@ -258,6 +260,73 @@ int32_t cf_paged_write(const CfTensor* x_new, const CfTensor* slot_mapping,
  *   out           [R, S, H, D]     f32 | f16 | bf16, any strides */
 int32_t cf_paged_gather(const CfTensor* cache, const CfTensor* block_tables,
                         const CfTensor* scale, CfTensor* out, void* stream);
+
+/* ---- Paged block pool (host) ---------------------------------------------
+ * Replaces the reference's BlockManager (runtime/src/cache/block.rs:78-352;
+ * Python binding PyBlockManager, runtime/src/lib.rs:82-168): reference-
+ * counted physical blocks and per-request tables, same allocation order
+ * (free list = stack initialised 0..n-1, taken from and returned to its
+ * end), same error cases.  Handles are not thread-safe.  List outputs go to
+ * caller buffers of `cap` entries; *n_out receives the full count (pass a
+ * NULL buffer to query it).  Errors: CF_ERR_OUT_OF_BLOCKS (pool exhausted;
+ * also a duplicate id in cf_bp_allocate, as the reference reports it),
+ * CF_ERR_NOT_FOUND (unknown request), CF_ERR_INVALID. */
+int32_t cf_bp_create(int64_t num_blocks, int64_t block_size, void** out);
+int32_t cf_bp_destroy(void* pool);
+int32_t cf_bp_num_free(void* pool, int64_t* out);
+int32_t cf_bp_ref_count(void* pool, int64_t block_id, int64_t* out);
+/* BlockManager::allocate (block.rs:145-173). */
+int32_t cf_bp_allocate(void* pool, const char* request_id, int64_t num_tokens,
+                       int32_t* out, int64_t cap, int64_t* n_out);
+/* BlockManager::free (block.rs:177-196); also releases the request's device row. */
+int32_t cf_bp_free(void* pool, const char* request_id);
+/* BlockManager::free_block (block.rs:199-210). */
+int32_t cf_bp_free_block(void* pool, int64_t block_id);
+/* BlockManager::increment_ref_count (block.rs:321-325). */
+int32_t cf_bp_increment_ref_count(void* pool, int64_t block_id);
+/* BlockManager::assign_cached_blocks (block.rs:214-231). */
+int32_t cf_bp_assign_cached_blocks(void* pool, const char* request_id,
+                                   const int32_t* block_ids, int64_t n);
+/* BlockManager::ensure_blocks (block.rs:235-266). */
+int32_t cf_bp_ensure_blocks(void* pool, const char* request_id, int64_t target_tokens);
+/* BlockManager::share_prefix (block.rs:271-303). */
+int32_t cf_bp_share_prefix(void* pool, const char* src_request_id, const char* dst_request_id,
+                           int64_t prefix_len, int32_t* out, int64_t cap, int64_t* n_out);
+/* BlockManager::get_blocks (block.rs:307-312). */
+int32_t cf_bp_get_blocks(void* pool, const char* request_id, int32_t* out, int64_t cap,
+                         int64_t* n_out);
+/* No reference counterpart (the reference writes into shared blocks, the
+ * hazard of a shared partial block).  For each request i, makes the blocks
+ * holding positions [start[i], start[i] + count[i]) its own: the table grows
+ * to cover them, then each touched block with reference count > 1 is
+ * replaced by a fresh block and (old, new) is appended to copies
+ * ([copies_cap][2]) for cf_copy_blocks.  slots (sum of count) receives each
+ * token's block * block_size + offset.  All-or-nothing on exhaustion. */
+int32_t cf_bp_prepare_writes(void* pool, int64_t n_requests, const char* const* request_ids,
+                             const int64_t* start, const int64_t* count, int64_t* slots,
+                             int32_t* copies, int64_t copies_cap, int64_t* n_copies);
+/* Sets a request's token count (its device row length). */
+int32_t cf_bp_set_len(void* pool, const char* request_id, int64_t tokens);
+/* Device-resident tables (no reference counterpart; the reference builds
+ * tables on the host every step).  cf_bp_bind_rows sizes the device table
+ * [rows, cols] (initialised to -1 by the caller) and lengths [rows];
+ * cf_bp_table_deltas lists the cells that changed since its last call as
+ * [n][4] = {row, col, value, 0} (col = -1: the row's length), assigning a
+ * row to each new request and zeroing freed requests' lengths;
+ * cf_block_tables_apply scatters them on the device. */
+int32_t cf_bp_bind_rows(void* pool, int32_t rows, int32_t cols);
+int32_t cf_bp_row_of(void* pool, const char* request_id, int32_t* row);
+int32_t cf_bp_table_deltas(void* pool, int32_t* deltas, int64_t cap, int64_t* n_out);
+/* Per device row: leading tokens it shares (same physical blocks) with the
+ * row before, capped by both lengths -- the decode kernel's shared-prefix
+ * statement (cf_paged_decode_shared). */
+int32_t cf_bp_shared_prefix_lens(void* pool, int32_t* out, int64_t rows);
+int32_t cf_block_tables_apply(CfTensor* table, CfTensor* lens, const CfTensor* deltas,
+                              void* stream);
+/* Copies whole blocks of a paged cache viewed as [NB, E] (a block's E
+ * elements contiguous, E stride 1): block pairs[i][1] <- pairs[i][0], for
+ * copy-on-write.  A destination must not be another pair's source. */
+int32_t cf_copy_blocks(CfTensor* cache, const CfTensor* pairs, void* stream);
 
 /* Kernel timing hook for benchmarks (no reference counterpart).  While
  * enabled, every kernel this library launches is bracketed by a pair of

@@ -36,6 +36,8 @@ CF_ERR_INVALID = -1
 CF_ERR_HIP = -2
 CF_ERR_WORKSPACE = -3
 CF_ERR_UNSUPPORTED = -4
+CF_ERR_OUT_OF_BLOCKS = -5
+CF_ERR_NOT_FOUND = -6
 
 _DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: CF_F32,
@@ -161,6 +163,33 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "cf_kv_write_fp8": (ctypes.c_int32, [_P, _P, _P, _P, _P, _P, _P, ctypes.c_void_p]),
     "cf_paged_write": (ctypes.c_int32, [_P, _P, _P, _P, ctypes.c_void_p]),
     "cf_paged_gather": (ctypes.c_int32, [_P, _P, _P, _P, ctypes.c_void_p]),
+    "cf_bp_create": (ctypes.c_int32, [ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_void_p)]),
+    "cf_bp_destroy": (ctypes.c_int32, [ctypes.c_void_p]),
+    "cf_bp_num_free": (ctypes.c_int32, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64)]),
+    "cf_bp_ref_count": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
+    "cf_bp_allocate": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64, ctypes.c_void_p,
+                                        ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
+    "cf_bp_free": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p]),
+    "cf_bp_free_block": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int64]),
+    "cf_bp_increment_ref_count": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int64]),
+    "cf_bp_assign_cached_blocks": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p,
+                                                    ctypes.c_int64]),
+    "cf_bp_ensure_blocks": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64]),
+    "cf_bp_share_prefix": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int64,
+                                            ctypes.c_void_p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
+    "cf_bp_get_blocks": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_int64,
+                                          ctypes.POINTER(ctypes.c_int64)]),
+    "cf_bp_prepare_writes": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                              ctypes.POINTER(ctypes.c_int64)]),
+    "cf_bp_set_len": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64]),
+    "cf_bp_bind_rows": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32]),
+    "cf_bp_row_of": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int32)]),
+    "cf_bp_table_deltas": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                            ctypes.POINTER(ctypes.c_int64)]),
+    "cf_bp_shared_prefix_lens": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
+    "cf_block_tables_apply": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
+    "cf_copy_blocks": (ctypes.c_int32, [_P, _P, ctypes.c_void_p]),
     "cf_profile_enable": (ctypes.c_int32, [ctypes.c_int32]),
     "cf_profile_reset": (ctypes.c_int32, []),
     "cf_profile_query": (
@@ -208,6 +237,8 @@ def check(rc: int, what: str) -> None:
         raise ValueError(msg)
     if rc == CF_ERR_UNSUPPORTED:
         raise NotImplementedError(msg)
+    if rc == CF_ERR_NOT_FOUND:
+        raise KeyError(msg)
     raise RuntimeError(msg)
 
 

@@ -386,6 +386,47 @@ def paged_gather(
     return out
 
 
+def block_tables_apply(table: torch.Tensor, lens: torch.Tensor, deltas: torch.Tensor) -> None:
+    """Scatters block-table deltas [n, 4] int32 = {row, col, value, 0} into a
+    device table [rows, cols] int32 (col = -1: lens[row] = value)."""
+    for name, t in (("table", table), ("lens", lens), ("deltas", deltas)):
+        _require_device(name, t)
+    dev = _same_device(table, lens, deltas)
+    dt, dl, dd = descriptor(table), descriptor(lens), descriptor(deltas)
+    with torch.cuda.device(dev):
+        rc = lib().cf_block_tables_apply(ref(dt), ref(dl), ref(dd), stream_handle(dev))
+    check(rc, "cf_block_tables_apply")
+
+
+def block_span_view(cache: torch.Tensor) -> torch.Tensor:
+    """[NB, E] view of a paged tensor whose dim 0 is the block: raises unless
+    each block's elements fill one contiguous span."""
+    if cache.dim() < 1:
+        raise ValueError("cache must have a block dimension")
+    nb = cache.shape[0]
+    inner = [(n, st) for n, st in zip(cache.shape[1:], cache.stride()[1:]) if n > 1]
+    span = 1 + sum((n - 1) * st for n, st in inner)
+    elems = 1
+    for n, _ in inner:
+        elems *= n
+    if span != elems or (nb > 1 and cache.stride(0) < elems):
+        raise ValueError("cache blocks are not dense contiguous spans")
+    return torch.as_strided(cache, (nb, elems), (cache.stride(0) if nb > 1 else elems, 1), cache.storage_offset())
+
+
+def copy_blocks(cache: torch.Tensor, pairs: torch.Tensor) -> None:
+    """Copies whole blocks of a paged tensor (dim 0 = block): block
+    pairs[i, 1] <- block pairs[i, 0] (pairs int32 [n, 2] on the device)."""
+    _require_device("cache", cache)
+    _require_device("pairs", pairs)
+    dev = _same_device(cache, pairs)
+    flat = block_span_view(cache).view(torch.uint8)  # bytes: any element type
+    dc, dp = descriptor(flat), descriptor(pairs)
+    with torch.cuda.device(dev):
+        rc = lib().cf_copy_blocks(ref(dc), ref(dp), stream_handle(dev))
+    check(rc, "cf_copy_blocks")
+
+
 class KernelTimer:
     """Sums device time of this library's kernel launches (HIP events)."""
 
@@ -413,6 +454,9 @@ __all__ = [
     "DEFAULT_PARTITION_TOKENS",
     "DecodePlan",
     "KernelTimer",
+    "block_span_view",
+    "block_tables_apply",
+    "copy_blocks",
     "decode_workspace_bytes",
     "prefill_chunk",
     "prefill_workspace_bytes",

@@ -488,6 +488,57 @@ class CacheManager:
             q, kv, vv, tables, seq_t, float(scale), bs, k_scale=ks, v_scale=vs, out=out, shared_prefix_lens=sp_t
         )
 
+    def write_slots(self, slab_id: str, layer_idx: int, data: torch.Tensor, slots: torch.Tensor | np.ndarray) -> None:
+        """Writes token rows at explicit slots (block * block_size + offset),
+        e.g. those BlockManager.prepare_writes returns; negative slots are
+        skipped."""
+        spec = self._specs[slab_id]
+        rows = normalize_kv(data, spec.num_heads, spec.head_dim)
+        if rows.dim() != 3:
+            raise ValueError(f"write_slots: cannot read {tuple(data.shape)} as [seq, {spec.num_heads}, {spec.head_dim}]")
+        slots = torch.as_tensor(slots).reshape(-1).to(self._device)
+        if slots.numel() != rows.shape[0]:
+            raise ValueError(f"write_slots: {slots.numel()} slots for {rows.shape[0]} rows")
+        if rows.device != self._device:
+            rows = rows.to(self._device)
+        view = self.layer_view(slab_id, layer_idx)
+        if view.dtype == torch.float64:
+            bs = self._block_size
+            keep = slots >= 0
+            s = slots[keep]
+            view[s // bs, s % bs] = rows[keep].to(torch.float64)
+            return
+        sc = self._scales[slab_id][layer_idx] if slab_id in self._scales else None
+        _ops.paged_write(rows, slots, view, sc)
+
+    def attend_rows(
+        self,
+        q: torch.Tensor,
+        layer_idx: int,
+        block_tables: torch.Tensor,
+        seq_lens: torch.Tensor,
+        shared_prefix_lens: torch.Tensor | None = None,
+        k_slab: str = "k",
+        v_slab: str = "v",
+        scale: float | None = None,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Decode attention from the slabs with device-resident tables (e.g.
+        BlockManager.sync_device): q [rows, q_heads, dim], block_tables int32
+        [rows, cols], seq_lens int32 [rows] (rows of length 0 give zeros)."""
+        kv = self.layer_view(k_slab, layer_idx)
+        vv = self.layer_view(v_slab, layer_idx)
+        ks = self._scales[k_slab][layer_idx] if k_slab in self._scales else None
+        vs = self._scales[v_slab][layer_idx] if v_slab in self._scales else None
+        if scale is None:
+            scale = 1.0 / math.sqrt(q.shape[-1])
+        return _ops.paged_decode(q, kv, vv, block_tables, seq_lens, float(scale), self._block_size, k_scale=ks,
+                                 v_scale=vs, out=out, shared_prefix_lens=shared_prefix_lens)
+
+    def paged_slabs(self) -> list[torch.Tensor]:
+        """Every paged slab (all layers), e.g. for BlockManager.copy_blocks."""
+        return [t for name, t in self._slabs.items() if self._specs[name].slab_type == "paged"]
+
     # ── Fixed state I/O ──────────────────────────────────
 
     def write_fixed(self, slab_id: str, slot: int, layer_idx: int, data: torch.Tensor) -> None:
