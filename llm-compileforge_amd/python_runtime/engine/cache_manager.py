@@ -535,6 +535,32 @@ class CacheManager:
         return _ops.paged_decode(q, kv, vv, block_tables, seq_lens, float(scale), self._block_size, k_scale=ks,
                                  v_scale=vs, out=out, shared_prefix_lens=shared_prefix_lens)
 
+    def attend_chunks(
+        self,
+        q: torch.Tensor,
+        layer_idx: int,
+        block_tables: torch.Tensor,
+        seq_lens: torch.Tensor,
+        q_start: torch.Tensor,
+        k_slab: str = "k",
+        v_slab: str = "v",
+        scale: float | None = None,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Chunked-prefill attention from the slabs: q [Tq, q_heads, dim]
+        holds the rows of N chunks (chunk n owns rows [q_start[n],
+        q_start[n+1])), whose K/V are already written; row i of a chunk of L
+        rows sits at position seq_lens[n] - L + i and sees positions up to
+        it.  block_tables int32 [N, cols]; seq_lens int32 [N]."""
+        kv = self.layer_view(k_slab, layer_idx)
+        vv = self.layer_view(v_slab, layer_idx)
+        ks = self._scales[k_slab][layer_idx] if k_slab in self._scales else None
+        vs = self._scales[v_slab][layer_idx] if v_slab in self._scales else None
+        if scale is None:
+            scale = 1.0 / math.sqrt(q.shape[-1])
+        return _ops.prefill_chunk(q, kv, vv, block_tables, seq_lens, q_start, float(scale), self._block_size,
+                                  k_scale=ks, v_scale=vs, out=out)
+
     def paged_slabs(self) -> list[torch.Tensor]:
         """Every paged slab (all layers), e.g. for BlockManager.copy_blocks."""
         return [t for name, t in self._slabs.items() if self._specs[name].slab_type == "paged"]

@@ -189,3 +189,59 @@ def test_copy_on_write_decode_step(gpu):
     a_blk, b_blk = bm.get_blocks("A")[1], bm.get_blocks("B")[1]
     assert a_blk != b_blk and not np.array_equal(codes(kb[a_blk, 4]), codes(kb[b_blk, 4]))
     assert np.array_equal(codes(kb[a_blk, :4]), codes(kb[b_blk, :4]))  # the shared prefix rows were copied
+
+
+@pytest.mark.parametrize("dtype", ["float8_e4m3fn", "bfloat16"])
+def test_prefill_chunks_from_slabs(gpu, dtype):
+    """A chunked-prefill step through the block pool and CacheManager: two
+    requests with cached prefixes (one shared through the radix cache) write
+    their chunk's K/V at pool slots and attend from the slabs; the float64
+    oracle runs on the slab contents."""
+    from oracle.paged_attention import paged_prefill_fp64
+
+    L, hkv, g, d, bs = 2, 2, 4, 128, 16
+    mgr = CacheManager(CachePolicy.for_llama(L, hkv, d, kv_dtype=dtype), num_blocks=64, device=gpu)
+    bm = BlockManager(64, bs)
+    gen = torch.Generator().manual_seed(8)
+    if dtype == "float8_e4m3fn":
+        for name in ("k", "v"):
+            # |x| stays under ~12 (N(0, 2) rows): codes of x / scale stay finite (< 448)
+            mgr.set_kv_scales(name, torch.rand(L, hkv, generator=gen) * 0.02 + 0.05)
+
+    def rows(n):
+        return {(layer, name): (torch.randn(n, hkv, d, generator=gen) * 2).to(torch.bfloat16)
+                for layer in range(L) for name in ("k", "v")}
+
+    def write(writes, data):
+        slots, copies = bm.prepare_writes(writes)
+        BlockManager.copy_blocks(copies, mgr.paged_slabs())
+        for (layer, name), x in data.items():
+            mgr.write_slots(name, layer, x.to(gpu), slots)
+
+    # cached prefixes: A 37 tokens; B shares A's first 21 tokens (a partial block)
+    bm.allocate("A", 0)
+    write([("A", 0, 37)], rows(37))
+    bm.assign_cached_blocks("B", bm.get_blocks("A")[:2])
+    # this step's chunks: A +50 rows at 37.., B +70 rows at 21..
+    chunk = {"A": (37, 50), "B": (21, 70)}
+    write([(r, s, n) for r, (s, n) in chunk.items()], rows(120))
+    order = ["A", "B"]
+    tabs = [bm.get_blocks(r) for r in order]
+    width = max(len(t) for t in tabs)
+    tables = torch.tensor([t + [-1] * (width - len(t)) for t in tabs], dtype=torch.int32, device=gpu)
+    lens = torch.tensor([chunk[r][0] + chunk[r][1] for r in order], dtype=torch.int32, device=gpu)
+    q_start = torch.tensor([0, 50, 120], dtype=torch.int32, device=gpu)
+    q = torch.randn(120, hkv * g, d, generator=gen).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(d)
+    for layer in range(L):
+        got = mgr.attend_chunks(q.to(gpu), layer, tables, lens, q_start).float().cpu().numpy()
+        kc, vc = mgr.layer_view("k", layer).detach().cpu(), mgr.layer_view("v", layer).detach().cpu()
+        if dtype == "float8_e4m3fn":
+            kf, vf = ofp8.decode(codes(kc)), ofp8.decode(codes(vc))
+            ks, vs = mgr.kv_scales("k")[layer].cpu().numpy(), mgr.kv_scales("v")[layer].cpu().numpy()
+        else:
+            kf, vf, ks, vs = kc.float().numpy(), vc.float().numpy(), None, None
+        want, covered = paged_prefill_fp64(q.float().numpy(), kf, vf, tabs, lens.cpu().tolist(), [0, 50, 120], bs,
+                                           scale, ks, vs)
+        assert covered.all()
+        assert_close(got, want, torch.bfloat16, f"prefill from slabs {dtype} layer {layer}")
