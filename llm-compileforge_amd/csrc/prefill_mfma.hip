@@ -25,7 +25,13 @@
 // Per tile and column tile the math is the decode kernel's (decode_mfma.hip):
 // S^T = K Q^T as two 16-token MFMA chains, online softmax in log2 units
 // with lazy rescaling, O^T += V^T P^T; the K-row order inside the tile
-// makes each lane's scores exactly the P^T operand it feeds.
+// makes each lane's scores exactly the P^T operand it feeds.  The softmax
+// keeps cross-lane work off the common path: the rescale test is lane-local
+// (a column's max across its 4 lanes is taken only when some lane passes
+// the threshold), and the row sums come out of the MFMA pipe as one more
+// PV product against an all-ones V channel instead of per-score adds.
+// Staging threads take K operand entries lane-fastest so the LDS writes of
+// a wave are contiguous (no bank conflicts).
 //
 // Items come from a queue the plan kernel sorts longest first (counting
 // sort on the tile count), so the persistent workgroups finish together
@@ -182,7 +188,7 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
     const int u = tid + 256 * i;
     if (u < Gm::KU) {
       const int s = u / (64 * Gm::KUPL), rem = u % (64 * Gm::KUPL);
-      const int lane = rem / Gm::KUPL, cp = rem % Gm::KUPL;
+      const int lane = rem % 64, cp = rem / 64;
       const int li = lane & 15, lq = lane >> 4;
       const int row = ((8 * (li >> 2) + (li & 3)) & 15) + 4 * s;
       const int blk = li < 8 ? t.a : t.b;
@@ -219,7 +225,7 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
     const int u = tid + 256 * i;
     if (u < Gm::KU) {
       const int s = u / (64 * Gm::KUPL), rem = u % (64 * Gm::KUPL);
-      const int lane = rem / Gm::KUPL, cp = rem % Gm::KUPL;
+      const int lane = rem % 64, cp = rem / 64;
       if constexpr (KT == kE4M3) {
         lds[(s * Gm::NC + 2 * cp) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_bf16(kr[i].x, kr[i].y));
         lds[(s * Gm::NC + 2 * cp + 1) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_bf16(kr[i].z, kr[i].w));
@@ -229,6 +235,9 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
     }
   }
   uint4* vl = lds + Gm::KENT;
+  // Tiles whose 32 tokens are all valid (all but an item's last tile) skip
+  // the masking (a wave-uniform branch).
+  const bool full = valid >= 32 && t.va && t.vb;
 #pragma unroll
   for (int i = 0; i < Gm::VPT; ++i) {
     const int u = tid + 256 * i;
@@ -237,7 +246,14 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
       const int d = rem / Gm::VPER, part = rem % Gm::VPER;
       const bool ok = X ? t.vb : t.va;
       const int li = d & 15, tt = d >> 4;
-      if constexpr (KT == kE4M3) {
+      if (full) {
+        if constexpr (KT == kE4M3) {
+          vl[tt * 64 + 32 * X + li] = __builtin_bit_cast(uint4, e4m3x8_to_f16(vr[i].x, vr[i].y));
+          vl[tt * 64 + 32 * X + 16 + li] = __builtin_bit_cast(uint4, e4m3x8_to_f16(vr[i].z, vr[i].w));
+        } else {
+          vl[tt * 64 + 32 * X + 16 * part + li] = vr[i];
+        }
+      } else if constexpr (KT == kE4M3) {
         const int n0 = ok ? valid - 16 * X : 0;  // valid tokens among this load's 16
         const uint2 lo = keep_bytes(make_uint2(vr[i].x, vr[i].y), n0);
         const uint2 hi = keep_bytes(make_uint2(vr[i].z, vr[i].w), n0 - 8);
@@ -329,8 +345,11 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     // masked ones.
     if (qk_scale == 0.0f) qk_scale = 1.17549435e-38f;
 
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    float m[2] = {-INFINITY, -INFINITY};
     f32x4_t o[2][NV];
+    // Row sums come from the PV MFMAs: an extra V tile whose channel 0 is all
+    // ones gives O[column][0] = sum of P (lane (li, lq = 0), element 0).
+    f32x4_t ol[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
     for (int k = 0; k < 2; ++k)
 #pragma unroll
@@ -393,15 +412,16 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
           float mt = sc[0];
 #pragma unroll
           for (int v = 1; v < 8; ++v) mt = fmaxf(mt, sc[v]);
-          mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-          mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
           mt *= qk_scale;  // qk_scale > 0: the max of scaled scores (log2 units)
           // lazy rescale: the running max moves only when a score passes it
-          // by more than 8, so p <= 256
+          // by more than 8, so p <= 256.  The lane-local test decides; the
+          // column max (across the 4 lanes of a column) is taken only then.
           if (__any(mt > m[k] + 8.0f)) {
+            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
             const float mnew = mt > m[k] + 8.0f ? mt : m[k];
             const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[k] - mnew);
-            l[k] *= alpha;
+            ol[k] = ol[k] * alpha;
 #pragma unroll
             for (int t = 0; t < NV; ++t) o[k][t] = o[k][t] * alpha;
             m[k] = mnew;
@@ -409,11 +429,9 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
           // a column with nothing visible yet keeps m = -inf; its scores are
           // all -inf, so any finite reference gives p = 0
           const float mref = m[k] == -INFINITY ? 0.0f : m[k];
-          float psum = 0.0f;
 #pragma unroll
           for (int v = 0; v < 8; ++v) {
             const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], qk_scale, -mref));
-            psum += pv;
             if constexpr (KT == kE4M3) {
               pop[k][v] = (_Float16)pv;
             } else {
@@ -422,9 +440,21 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
               plo[k][v] = (__bf16)(pv - (float)hi);
             }
           }
-          l[k] += psum;
         }
         // ---- O^T += V^T P^T ------------------------------------------------
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          if constexpr (KT == kE4M3) {
+            const _Float16 one = li == 0 ? (_Float16)1.0f : (_Float16)0.0f;
+            const f16x8_t ones = {one, one, one, one, one, one, one, one};
+            ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[k], ol[k], 0, 0, 0);
+          } else {
+            const __bf16 one = li == 0 ? (__bf16)1.0f : (__bf16)0.0f;
+            const bf16x8_t ones = {one, one, one, one, one, one, one, one};
+            ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[k], ol[k], 0, 0, 0);
+            ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, plo[k], ol[k], 0, 0, 0);
+          }
+        }
 #pragma unroll
         for (int t = 0; t < NV; ++t) {
 #pragma unroll
@@ -455,8 +485,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     const float vs = vscale ? vscale[h * p.vs_s] : 1.0f;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      float lt = l[k] + __shfl_xor(l[k], 16, 64);
-      lt += __shfl_xor(lt, 32, 64);
+      const float lt = __shfl(ol[k][0], li, 64);  // lane (li, 0) holds column li's sum
       const int col = 32 * wave + 16 * k + li;
       const int r = col / G, g = col % G;
       if (r < rows) {
