@@ -536,13 +536,15 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     float mt = sc[0];
 #pragma unroll
     for (int v = 1; v < 8; ++v) mt = fmaxf(mt, sc[v]);
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     // Lazy rescaling: the running max moves only when a score exceeds it by
     // more than 8 (log2 units), so p = 2^(s - m) <= 256 -- exact enough in
     // fp16/bf16 operands and fp32 sums -- and the O rescale is skipped on
     // almost every tile.
     if (__any(mt > m + 8.0f)) {
+      // the lane-local test decides; the column max (across the 4 lanes of
+      // a column) is taken only then
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
       const float mnew = mt > m + 8.0f ? mt : m;
       const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
       l *= alpha;

@@ -178,31 +178,82 @@ __device__ __forceinline__ uint4 pack16(const uint32_t* b) {
 // token's K row, 16 V values into one byte of each of 16 V channel rows.
 // Codes are the same e4m3_from_f32(x / scale) as kv_write_kernel.
 template <int XT, int ST>
-__global__ __launch_bounds__(256) void kv_write_native_kernel(KvWriteParams p) {
+__device__ __forceinline__ int64_t slot_at(const KvWriteParams& p, int64_t i) {
+  return ST == kI64 ? ((const int64_t*)p.slots)[i * p.slot_stride]
+                    : (int64_t)((const int32_t*)p.slots)[i * p.slot_stride];
+}
+
+// Workgroups [0, k_blocks): K, one thread per (new row, head, 16-channel
+// piece): a 16-byte load, 16 conversions, one 16-byte store of the token's
+// K row piece.  Workgroups after that: V, one per (group of 16 new rows,
+// 256 channels of the H * D); each thread owns one (head, channel).  V is
+// channel-major in a block (16 tokens of a channel are 16 contiguous
+// bytes), so the rows are walked as runs of consecutive slots inside one
+// block: a run starting in the group is written by this workgroup (it may
+// extend past the group), a full block row as one 16-byte store, a partial
+// run as byte stores.  Run boundaries depend only on the slots, so every
+// thread of the workgroup walks the same runs.
+template <int XT, int ST>
+__global__ __launch_bounds__(256) void kv_write_native_kernel(KvWriteParams p, int64_t k_blocks, int v_chunks) {
   using XE = Elem<XT>;
   constexpr int EB = sizeof(typename XE::T);
-  const int nch = p.D / 16;
-  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (u >= p.T * p.H * nch) return;
-  const int c = (int)(u % nch), h = (int)((u / nch) % p.H);
-  const int64_t i = u / ((int64_t)nch * p.H);
-  const int64_t sl = ST == kI64 ? ((const int64_t*)p.slots)[i * p.slot_stride]
-                                : (int64_t)((const int32_t*)p.slots)[i * p.slot_stride];
-  if (sl < 0 || sl >= p.NB * 16) return;
-  const int64_t blk = sl >> 4;
-  const int off = (int)(sl & 15);
-  float f[16];
-  uint32_t b[16];
-  load16<XT>((const uint8_t*)p.k_new.base + (i * p.k_new.stride[1] + h * p.k_new.stride[2] + c * 16) * EB, f);
-  const float ks = p.k_scale[h * p.ks_s];
+  if ((int64_t)blockIdx.x < k_blocks) {
+    const int nch = p.D / 16;
+    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (u >= p.T * p.H * nch) return;
+    const int c = (int)(u % nch), h = (int)((u / nch) % p.H);
+    const int64_t i = u / ((int64_t)nch * p.H);
+    const int64_t sl = slot_at<XT, ST>(p, i);
+    if (sl < 0 || sl >= p.NB * 16) return;
+    const int64_t blk = sl >> 4;
+    const int off = (int)(sl & 15);
+    float f[16];
+    uint32_t b[16];
+    load16<XT>((const uint8_t*)p.k_new.base + (i * p.k_new.stride[1] + h * p.k_new.stride[2] + c * 16) * EB, f);
+    const float ks = p.k_scale[h * p.ks_s];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) b[e] = e4m3_from_f32(f[e] / ks);
-  *(uint4*)((uint8_t*)p.k_cache + blk * p.kc_s[0] + h * p.kc_s[2] + off * p.D + c * 16) = pack16(b);
-  load16<XT>((const uint8_t*)p.v_new.base + (i * p.v_new.stride[1] + h * p.v_new.stride[2] + c * 16) * EB, f);
+    for (int e = 0; e < 16; ++e) b[e] = e4m3_from_f32(f[e] / ks);
+    *(uint4*)((uint8_t*)p.k_cache + blk * p.kc_s[0] + h * p.kc_s[2] + off * p.D + c * 16) = pack16(b);
+    return;
+  }
+  const int64_t vb = (int64_t)blockIdx.x - k_blocks;
+  const int64_t g = vb / v_chunks;
+  const int hd = (int)(vb % v_chunks) * 256 + (int)threadIdx.x;
+  const bool mine = hd < p.H * p.D;
+  const int h = mine ? hd / p.D : 0, d = mine ? hd % p.D : 0;
   const float vs = p.v_scale[h * p.vs_s];
-  uint8_t* vrow = (uint8_t*)p.v_cache + blk * p.vc_s[0] + h * p.vc_s[2] + (c * 16) * 16 + off;
+  const int64_t cap = p.NB * 16;
+  // lane l holds the slot of row g * 16 - 1 + l (-1 outside [0, T)): the
+  // group's 16 rows, the row before and enough rows after for any run
+  const int lane = (int)(threadIdx.x & 63);
+  const int64_t r = g * 16 - 1 + lane;
+  const int64_t sl = r >= 0 && r < p.T ? slot_at<XT, ST>(p, r) : -1;
+  const bool valid = sl >= 0 && sl < cap;
+  const int64_t up = __shfl_up(sl, 1, 64);
+  // cont: this row takes the slot after the previous row's, in the same block
+  const bool cont = valid && lane > 0 && sl == up + 1 && (sl & 15) != 0;
+  uint64_t starts = __ballot(valid && !cont && lane >= 1 && lane <= 16);
+  const uint64_t conts = __ballot(cont);
+  while (starts) {
+    const int st = __builtin_ctzll(starts);
+    starts &= starts - 1;
+    const int n = 1 + __builtin_ctzll(~(conts >> (st + 1)));  // run length (<= 16: runs stop at a block end)
+    const int64_t s0 = ((int64_t)__shfl(sl, st, 64));
+    const int64_t i = g * 16 - 1 + st;
+    if (!mine) continue;
+    uint8_t* vrow = (uint8_t*)p.v_cache + (s0 >> 4) * p.vc_s[0] + h * p.vc_s[2] + d * 16;
+    const typename XE::T* src =
+        (const typename XE::T*)p.v_new.base + i * p.v_new.stride[1] + (int64_t)h * p.v_new.stride[2] + d;
+    if (n == 16) {
+      uint32_t b[16];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) vrow[e * 16] = e4m3_from_f32(f[e] / vs);
+      for (int e = 0; e < 16; ++e) b[e] = e4m3_from_f32(XE::load(src + e * p.v_new.stride[1]) / vs);
+      *(uint4*)vrow = pack16(b);
+    } else {
+      const int o0 = (int)(s0 & 15);
+      for (int e = 0; e < n; ++e) vrow[o0 + e] = e4m3_from_f32(XE::load(src + e * p.v_new.stride[1]) / vs);
+    }
+  }
 }
 
 // Whether kv_write_native_kernel applies: native cache layout with block
@@ -445,9 +496,14 @@ int32_t launch_dequantize(const Rank4& q, const float* scales, int64_t s_stride,
 int32_t launch_kv_write_fp8(const KvWriteParams& p, int x_dt, int slot_dt, hipStream_t stream) {
   if (p.T == 0) return CF_OK;
   if (kv_write_native_ok(p, x_dt)) {
-    const dim3 grid((unsigned)ceil_div(p.T * p.H * (p.D / 16), 256));
+    const int64_t k_blocks = ceil_div(p.T * p.H * (p.D / 16), 256);
+    const int v_chunks = (int)ceil_div((int64_t)p.H * p.D, 256);
+    const int64_t blocks = k_blocks + ceil_div(p.T, 16) * v_chunks;
+    CF_CHECK(blocks < (int64_t)INT32_MAX, "kv_write: too many rows");
+    const dim3 grid((unsigned)blocks);
     ProfileScope prof("cf_kv_write_fp8", stream);
-#define CF_KVN(XT, ST) hipLaunchKernelGGL((kv_write_native_kernel<XT, ST>), grid, dim3(256), 0, stream, p)
+#define CF_KVN(XT, ST) \
+  hipLaunchKernelGGL((kv_write_native_kernel<XT, ST>), grid, dim3(256), 0, stream, p, k_blocks, v_chunks)
     switch (x_dt * 8 + (slot_dt == kI64 ? 1 : 0)) {
       case kF32 * 8: CF_KVN(kF32, kI32); break;
       case kF32 * 8 + 1: CF_KVN(kF32, kI64); break;

@@ -115,3 +115,42 @@ def test_kv_write_bit_exact(gpu, layout, slot_dtype):
         assert np.array_equal(kcodes[s // bs, s % bs], wk[i])
         assert np.array_equal(vcodes[s // bs, s % bs], wv[i])
     assert np.all(kcodes[~written] == 0xAA) and np.all(vcodes[~written] == 0xAA)
+
+
+@pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("h,d", [(8, 128), (3, 64)])
+def test_kv_write_runs_bit_exact(gpu, slot_dtype, h, d):
+    """Slot patterns of a mixed step on the native layout: chunks starting
+    mid-block (runs crossing the kernel's 16-row groups), whole blocks,
+    partial last blocks, single decode tokens, invalid slots inside a run,
+    and consecutive slots crossing a block boundary."""
+    nb, bs = 64, 16
+    gen = torch.Generator().manual_seed(5)
+    slots: list[int] = []
+    slots += list(range(5 * bs + 7, 5 * bs + 7 + 45))  # chunk from mid-block 5 into blocks 6, 7, 8
+    slots += list(range(20 * bs, 20 * bs + 32))  # two whole blocks
+    slots += [33 * bs + 3, 40 * bs + 15, 41 * bs]  # decode tokens; 40:15 -> 41:0 crosses a block
+    slots += list(range(50 * bs + 2, 50 * bs + 13))  # partial run
+    slots += [-1, 52 * bs + 1, 52 * bs + 2, -1, 52 * bs + 4]  # holes
+    slots += list(range(60 * bs, 60 * bs + 16))  # one more whole block, unaligned to the row groups
+    t = len(slots)
+    kc, vc = L.alloc_kv_cache(nb, bs, h, d, torch.float8_e4m3fn, gpu, "native")
+    kc.view(torch.uint8).fill_(0xAA)
+    vc.view(torch.uint8).fill_(0xAA)
+    k_new = torch.randn(t, h, d, generator=gen).to(torch.bfloat16).to(gpu)
+    v_new = torch.randn(t, h, d, generator=gen).to(torch.bfloat16).to(gpu)
+    ks = ops.fp8_amax_scale(k_new)
+    vs = ops.fp8_amax_scale(v_new)
+    FP8KVCacheQuantizer.write_kv_fp8(k_new, v_new, torch.tensor(slots, dtype=slot_dtype, device=gpu), kc, vc, ks, vs)
+    torch.cuda.synchronize()
+    kcodes, vcodes = codes(kc), codes(vc)
+    wk = ofp8.quantize_per_head(k_new.float().cpu().numpy())[0]
+    wv = ofp8.quantize_per_head(v_new.float().cpu().numpy())[0]
+    written = np.zeros((nb, bs), dtype=bool)
+    for i, s in enumerate(slots):
+        if s < 0:
+            continue
+        written[s // bs, s % bs] = True
+        assert np.array_equal(kcodes[s // bs, s % bs], wk[i]), (i, s)
+        assert np.array_equal(vcodes[s // bs, s % bs], wv[i]), (i, s)
+    assert np.all(kcodes[~written] == 0xAA) and np.all(vcodes[~written] == 0xAA)
