@@ -18,11 +18,51 @@ Added, backward-compatible:
 
 from __future__ import annotations
 
+import array
 import math
+
+import numpy as np
 
 import torch
 
 from cf_hip import ops as _ops
+
+# Pinned staging for the dict API's tables / lengths / shared-prefix
+# statement: two buffers per device, each reused once the copy that last
+# read it has run (an event per buffer), so a call allocates no pinned
+# memory and never waits on the GPU in steady state.
+_STAGE: dict[torch.device, list] = {}
+
+
+def _as_ids(blocks) -> np.ndarray:
+    """Block ids as int64 (Python lists unboxed through array.array, the
+    fastest route; anything else through numpy)."""
+    if isinstance(blocks, list):
+        try:
+            return np.frombuffer(array.array("q", blocks), dtype=np.int64)
+        except (TypeError, OverflowError):
+            pass
+    if isinstance(blocks, torch.Tensor):
+        blocks = blocks.detach().cpu()
+    return np.asarray(blocks, dtype=np.int64)
+
+
+def _staging(device: torch.device, n: int) -> torch.Tensor:
+    st = _STAGE.setdefault(device, [[None, None], [None, None], 0])
+    bufs, events, k = st
+    if events[k] is not None:
+        events[k].synchronize()
+    if bufs[k] is None or bufs[k].numel() < n:
+        bufs[k] = torch.empty(max(n, 1 << 16), dtype=torch.int32, pin_memory=True)
+    return bufs[k]
+
+
+def _staged(device: torch.device) -> None:
+    st = _STAGE[device]
+    ev = torch.cuda.Event()
+    ev.record(torch.cuda.current_stream(device))
+    st[1][st[2]] = ev
+    st[2] ^= 1
 
 DEFAULT_PARTITION_TOKENS = _ops.DEFAULT_PARTITION_TOKENS
 
@@ -123,39 +163,52 @@ def paged_attention(
     rids = list(block_tables.keys())
     if len(rids) > q.shape[0]:
         raise IndexError(f"{len(rids)} requests but q holds {q.shape[0]} rows")
+    if not rids:
+        return {}
     nb = k_cache.shape[0]
-    lens: list[int] = []
-    tables: list[list[int]] = []
-    for rid in rids:
+    n_req = len(rids)
+    used: list[np.ndarray] = []
+    nblk = np.empty(n_req, dtype=np.int64)
+    lens = np.empty(n_req, dtype=np.int64)
+    for i, rid in enumerate(rids):
         blocks = block_tables[rid]
         seq_len = seq_lens.get(rid, len(blocks) * block_size)
         n_blocks = min(len(blocks), (seq_len + block_size - 1) // block_size)
         if n_blocks <= 0:
             # The reference fails here too (torch.cat of an empty list).
             raise RuntimeError(f"request {rid!r}: no KV blocks to attend (seq_len={seq_len})")
-        used = []
-        for bid in blocks[:n_blocks]:
-            bid = int(bid)
-            if not -nb <= bid < nb:
-                raise IndexError(f"request {rid!r}: block id {bid} out of range for {nb} cache blocks")
-            used.append(bid + nb if bid < 0 else bid)
-        tables.append(used)
-        lens.append(min(seq_len, n_blocks * block_size))
-    if not rids:
-        return {}
-    mb = max(len(t) for t in tables)
-    host_tables = torch.zeros(len(rids), mb, dtype=torch.int32, pin_memory=True)
-    for i, t in enumerate(tables):
-        host_tables[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
-    host_lens = torch.tensor(lens, dtype=torch.int32).pin_memory()
+        used.append(_as_ids(blocks[:n_blocks]))
+        nblk[i] = n_blocks
+        lens[i] = min(seq_len, n_blocks * block_size)
+    mb = int(nblk.max())
+    mat = np.zeros((n_req, mb), dtype=np.int64)
+    for i, u in enumerate(used):
+        mat[i, : u.shape[0]] = u
+    live = np.arange(mb)[None, :] < nblk[:, None]
+    bad = live & ((mat < -nb) | (mat >= nb))
+    if bad.any():
+        i, j = np.argwhere(bad)[0]
+        raise IndexError(f"request {rids[i]!r}: block id {int(mat[i, j])} out of range for {nb} cache blocks")
+    mat = np.where(mat < 0, mat + nb, mat)
     # Blocks shared between neighbouring requests (radix-cache prefixes) are
-    # read once per group of sharers.
-    host_shared = torch.tensor(_ops.shared_prefix_lens(tables, lens, block_size), dtype=torch.int32).pin_memory()
-    dev_tables = host_tables.to(q.device, non_blocking=True)
-    dev_lens = host_lens.to(q.device, non_blocking=True)
-    dev_shared = host_shared.to(q.device, non_blocking=True)
+    # read once per group of sharers: leading equal table entries, in tokens,
+    # cut to both lengths (cf_hip.ops.shared_prefix_lens, vectorized).
+    shared = np.zeros(n_req, dtype=np.int64)
+    if n_req > 1:
+        same = (mat[1:] == mat[:-1]) & live[1:] & live[:-1]
+        lead = np.cumprod(same, axis=1).sum(axis=1)
+        shared[1:] = np.maximum(0, np.minimum(np.minimum(lead * block_size, lens[:-1]), lens[1:]))
+    host = _staging(q.device, n_req * (mb + 2))
+    host[: n_req * mb].view(n_req, mb).numpy()[:] = mat
+    host[n_req * mb: n_req * (mb + 1)].numpy()[:] = lens
+    host[n_req * (mb + 1): n_req * (mb + 2)].numpy()[:] = shared
+    dev = host[: n_req * (mb + 2)].to(q.device, non_blocking=True)
+    _staged(q.device)
+    dev_tables = dev[: n_req * mb].view(n_req, mb)
+    dev_lens = dev[n_req * mb: n_req * (mb + 1)]
+    dev_shared = dev[n_req * (mb + 1):]
     out = paged_attention_tensors(
-        q[: len(rids)], k_cache, v_cache, dev_tables, dev_lens, block_size, scale,
+        q[:n_req], k_cache, v_cache, dev_tables, dev_lens, block_size, scale,
         k_scale=k_scale, v_scale=v_scale, partition_tokens=partition_tokens, shared_prefix_lens=dev_shared,
     )
     return {rid: out[i] for i, rid in enumerate(rids)}
