@@ -639,6 +639,68 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
   const int npre = dp.y < 0 ? 1 : dp.y;
   const int nsrc = nown + npre;
   if (nsrc == 0) return;  // written whole by the decode kernel (or empty)
+  constexpr int KMAX = 64 / E;  // partials the register path holds
+  if (nsrc <= KMAX) {
+    // Few partials (the usual case): every load is issued at once -- each
+    // lane's slice of every partial row and every (m, l) -- so the merge
+    // costs one round trip after the descriptors.
+    float ov[KMAX][E], mk[KMAX][G], lk[KMAX][G];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (k < nsrc) {
+        const int64_t row = k < nown ? part_row(dn, k) : part_row(dp, k - nown);
+        const float* o = p.ws_o + row * D;
+#pragma unroll
+        for (int i = 0; i < E; ++i) ov[k][i] = o[lane + 64 * i];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float2 ml = *(const float2*)(p.ws_ml + (row + g) * 2);
+          mk[k][g] = ml.x;
+          lk[k][g] = ml.y;
+        }
+      }
+    }
+    float Mg[G], Lg[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      Mg[g] = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k)
+        if (k < nsrc) Mg[g] = fmaxf(Mg[g], mk[k][g]);
+      Lg[g] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        if (k < nsrc) {
+          const float w = mk[k][g] == -INFINITY ? 0.0f : __expf(mk[k][g] - Mg[g]);
+          mk[k][g] = w;  // now the weight
+          Lg[g] += w * lk[k][g];
+        }
+      }
+    }
+    uint16_t* out = (uint16_t*)p.out + (int64_t)b * p.o_sb;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int idx = lane + 64 * i;
+      const int g = idx / D, d = idx % D;
+      float a = 0.0f;
+      float lg = 0.0f;
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg)
+        if (gg == g) lg = Lg[gg];
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        if (k < nsrc) {
+          float w = 0.0f;
+#pragma unroll
+          for (int gg = 0; gg < G; ++gg)
+            if (gg == g) w = mk[k][gg];
+          a += w * ov[k][i];
+        }
+      }
+      out[(int64_t)(h * G + g) * p.o_sh + d] = bf16_bits_from_f32(lg > 0.0f ? a / lg : 0.0f);
+    }
+    return;
+  }
   float acc[E];
 #pragma unroll
   for (int i = 0; i < E; ++i) acc[i] = 0.0f;
