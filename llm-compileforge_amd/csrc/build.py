@@ -14,6 +14,7 @@ from __future__ import annotations
 import argparse
 import os
 import subprocess
+import sysconfig
 import sys
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
@@ -78,7 +79,20 @@ def build(jobs: int = 8, verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
+    build_tablepack()
     return LIB
+
+
+def build_tablepack() -> Path:
+    """The CPython extension that packs paged_attention's request dicts
+    (host code, gcc, in-tree next to the ctypes binding)."""
+    src = PKG / "cf_hip" / "_tablepack.c"
+    out = PKG / "cf_hip" / ("_tablepack" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    _run(["gcc", "-O2", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}", str(src), "-o",
+          str(tmp)])
+    os.replace(tmp, out)
+    return out
 
 
 def main() -> None:

@@ -34,6 +34,59 @@ from cf_hip import ops as _ops
 _STAGE: dict[torch.device, list] = {}
 
 
+def _pack_tables_py(block_tables: dict, seq_lens: dict, block_size: int, nb: int, out: np.ndarray,
+                    width: int) -> int:
+    """pack_tables in numpy (used when the _tablepack extension is not built)."""
+    rids = list(block_tables.keys())
+    n_req = len(rids)
+    used: list[np.ndarray] = []
+    nblk = np.empty(n_req, dtype=np.int64)
+    lens = np.empty(n_req, dtype=np.int64)
+    for i, rid in enumerate(rids):
+        blocks = block_tables[rid]
+        seq_len = seq_lens.get(rid, len(blocks) * block_size)
+        n_blocks = min(len(blocks), (seq_len + block_size - 1) // block_size)
+        if n_blocks <= 0:
+            raise RuntimeError(f"request {rid!r}: no KV blocks to attend (seq_len={seq_len})")
+        used.append(_as_ids(blocks[:n_blocks]))
+        nblk[i] = n_blocks
+        lens[i] = min(seq_len, n_blocks * block_size)
+    mb = int(nblk.max())
+    mat = np.zeros((n_req, mb), dtype=np.int64)
+    for i, u in enumerate(used):
+        mat[i, : u.shape[0]] = u
+    live = np.arange(mb)[None, :] < nblk[:, None]
+    bad = live & ((mat < -nb) | (mat >= nb))
+    if bad.any():
+        i, j = np.argwhere(bad)[0]
+        raise IndexError(f"request {rids[i]!r}: block id {int(mat[i, j])} out of range for {nb} cache blocks")
+    mat = np.where(mat < 0, mat + nb, mat)
+    shared = np.zeros(n_req, dtype=np.int64)
+    if n_req > 1:
+        same = (mat[1:] == mat[:-1]) & live[1:] & live[:-1]
+        lead = np.cumprod(same, axis=1).sum(axis=1)
+        shared[1:] = np.maximum(0, np.minimum(np.minimum(lead * block_size, lens[:-1]), lens[1:]))
+    out[: n_req * mb] = mat.reshape(-1)
+    out[n_req * mb: n_req * (mb + 1)] = lens
+    out[n_req * (mb + 1): n_req * (mb + 2)] = shared
+    return mb
+
+
+try:  # the CPython packer next to the ctypes binding (built by csrc/build.py)
+    from cf_hip._tablepack import pack as _pack_native
+except ImportError:  # pragma: no cover - exercised when only the HIP library is built
+    _pack_native = None
+
+
+def pack_tables(block_tables: dict, seq_lens: dict, block_size: int, nb: int, out: np.ndarray, width: int) -> int:
+    """Request dicts -> int32 out[: n * (mb + 2)] = tables [n, mb] | lengths
+    [n] | shared-prefix lengths [n] (the reference's rules,
+    kernels/paged_attention.py:36-48; negative ids wrapped); returns mb."""
+    if _pack_native is not None:
+        return _pack_native(block_tables, seq_lens, int(block_size), int(nb), out, int(width))
+    return _pack_tables_py(block_tables, seq_lens, block_size, nb, out, width)
+
+
 def _as_ids(blocks) -> np.ndarray:
     """Block ids as int64 (Python lists unboxed through array.array, the
     fastest route; anything else through numpy)."""
@@ -167,41 +220,9 @@ def paged_attention(
         return {}
     nb = k_cache.shape[0]
     n_req = len(rids)
-    used: list[np.ndarray] = []
-    nblk = np.empty(n_req, dtype=np.int64)
-    lens = np.empty(n_req, dtype=np.int64)
-    for i, rid in enumerate(rids):
-        blocks = block_tables[rid]
-        seq_len = seq_lens.get(rid, len(blocks) * block_size)
-        n_blocks = min(len(blocks), (seq_len + block_size - 1) // block_size)
-        if n_blocks <= 0:
-            # The reference fails here too (torch.cat of an empty list).
-            raise RuntimeError(f"request {rid!r}: no KV blocks to attend (seq_len={seq_len})")
-        used.append(_as_ids(blocks[:n_blocks]))
-        nblk[i] = n_blocks
-        lens[i] = min(seq_len, n_blocks * block_size)
-    mb = int(nblk.max())
-    mat = np.zeros((n_req, mb), dtype=np.int64)
-    for i, u in enumerate(used):
-        mat[i, : u.shape[0]] = u
-    live = np.arange(mb)[None, :] < nblk[:, None]
-    bad = live & ((mat < -nb) | (mat >= nb))
-    if bad.any():
-        i, j = np.argwhere(bad)[0]
-        raise IndexError(f"request {rids[i]!r}: block id {int(mat[i, j])} out of range for {nb} cache blocks")
-    mat = np.where(mat < 0, mat + nb, mat)
-    # Blocks shared between neighbouring requests (radix-cache prefixes) are
-    # read once per group of sharers: leading equal table entries, in tokens,
-    # cut to both lengths (cf_hip.ops.shared_prefix_lens, vectorized).
-    shared = np.zeros(n_req, dtype=np.int64)
-    if n_req > 1:
-        same = (mat[1:] == mat[:-1]) & live[1:] & live[:-1]
-        lead = np.cumprod(same, axis=1).sum(axis=1)
-        shared[1:] = np.maximum(0, np.minimum(np.minimum(lead * block_size, lens[:-1]), lens[1:]))
-    host = _staging(q.device, n_req * (mb + 2))
-    host[: n_req * mb].view(n_req, mb).numpy()[:] = mat
-    host[n_req * mb: n_req * (mb + 1)].numpy()[:] = lens
-    host[n_req * (mb + 1): n_req * (mb + 2)].numpy()[:] = shared
+    width = max(len(t) for t in block_tables.values())
+    host = _staging(q.device, n_req * (width + 2))
+    mb = pack_tables(block_tables, seq_lens, block_size, nb, host.numpy(), width)
     dev = host[: n_req * (mb + 2)].to(q.device, non_blocking=True)
     _staged(q.device)
     dev_tables = dev[: n_req * mb].view(n_req, mb)
@@ -211,7 +232,7 @@ def paged_attention(
         q[:n_req], k_cache, v_cache, dev_tables, dev_lens, block_size, scale,
         k_scale=k_scale, v_scale=v_scale, partition_tokens=partition_tokens, shared_prefix_lens=dev_shared,
     )
-    return {rid: out[i] for i, rid in enumerate(rids)}
+    return dict(zip(rids, out.unbind(0)))
 
 
 def chunked_prefill_attention(
