@@ -328,6 +328,16 @@ int32_t cf_block_tables_apply(CfTensor* table, CfTensor* lens, const CfTensor* d
  * copy-on-write.  A destination must not be another pair's source. */
 int32_t cf_copy_blocks(CfTensor* cache, const CfTensor* pairs, void* stream);
 
+/* HBM read probe for measurement (no reference counterpart): `waves`
+ * independent waves (a multiple of 4) each read chunks_per_wave whole
+ * chunks of chunk_bytes at chunk_ids[w * chunks_per_wave + i] of buf (ids
+ * in [0, buf_bytes / chunk_bytes), trusted); `sink` (waves * 64 u32) is
+ * practically never written.  Gives the practical read rate for the decode
+ * kernel's access shape. */
+int32_t cf_hbm_read_probe(const void* buf, int64_t buf_bytes, const int32_t* chunk_ids,
+                          int64_t waves, int64_t chunks_per_wave, int64_t chunk_bytes,
+                          uint32_t* sink, void* stream);
+
 /* Kernel timing hook for benchmarks (no reference counterpart).  While
  * enabled, every kernel this library launches is bracketed by a pair of
  * HIP events recorded on the launch stream.  cf_profile_query synchronizes
