@@ -427,10 +427,14 @@ def main() -> None:
     dict_us = (time.perf_counter() - t0) * 1e6 / n_dict
     log(f"dict API: {dict_us:.1f} us/call, host {host_s * 1e6 / n_dict:.1f} us/call")
 
+    short = {torch.float8_e4m3fn: ("FP8", "e4m3"), torch.bfloat16: ("BF16", "bf16"), torch.float16: ("FP16", "f16"),
+             torch.float32: ("FP32", "f32")}
+    kv_name, kv_short = short[case.kv_dtype]
+    q_short = short[case.q.dtype][1]
     result = {
         # BASELINE.json's metric for its config (c3); other configs name theirs
         "metric": METRIC if args.config == "c3_llama3_8b" else
-        f"paged-decode tokens/s + HBM GB/s (% peak), {args.config} FP8 KV, 1 MI355X",
+        f"paged-decode tokens/s + HBM GB/s (% peak), {args.config} {kv_name} KV, 1 MI355X",
         "value": case.batch / (ms_step / 1e3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -440,7 +444,7 @@ def main() -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "e4m3 KV / bf16 q / f32 accumulate",
+        "dtype": f"{kv_short} KV / {q_short} q / f32 accumulate",
         "data": "synthetic (seeded), random-init",
         "config": {
             "workload": args.config,

@@ -142,34 +142,71 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
 
 // Merges the partition partials of one (sequence, query head):
 // O = sum_i exp(m_i - M) o_i / sum_i exp(m_i - M) l_i with M = max_i m_i.
+// 256 threads: (m, l) are read lane-parallel and reduced across the block;
+// the weighted sum takes the partitions in 256 / D interleaved groups (all
+// their loads independent), whose sums meet in LDS.
 template <int OT>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
+  __shared__ float red[8];
+  __shared__ float part_acc[256];
   const int hq = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
   const int ctx = effective_len(p, b);
   const int nparts = (ctx + p.PT - 1) / p.PT;
   using OutE = Elem<OT>;
   typename OutE::T* o = (typename OutE::T*)p.out + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
   const int64_t row0 = ((int64_t)b * p.Hq + hq) * p.max_parts;
+  const float* ml = p.ws_ml + row0 * 2;
+  const float* po = p.ws_o + row0 * p.D;
   if (nparts == 0) {
-    for (int d = threadIdx.x; d < p.D; d += blockDim.x) OutE::store(o + d, 0.0f);
+    for (int d = tid; d < p.D; d += 256) OutE::store(o + d, 0.0f);
     return;
   }
-  float M = -INFINITY;
-  for (int i = 0; i < nparts; ++i) M = fmaxf(M, p.ws_ml[(row0 + i) * 2]);
+  float mloc = -INFINITY;
+  for (int i = tid; i < nparts; i += 256) mloc = fmaxf(mloc, ml[i * 2]);
+  mloc = wave_max(mloc);
+  if (lane == 0) red[wave] = mloc;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   // A partition whose blocks were all invalid has m = -inf and l = 0.
-  float L = 0.0f;
-  for (int i = 0; i < nparts; ++i) {
-    const float m = p.ws_ml[(row0 + i) * 2];
-    if (m != -INFINITY) L += p.ws_ml[(row0 + i) * 2 + 1] * expf(m - M);
+  float lloc = 0.0f;
+  for (int i = tid; i < nparts; i += 256) {
+    const float m = ml[i * 2];
+    if (m != -INFINITY) lloc += ml[i * 2 + 1] * expf(m - M);
   }
+  lloc = wave_sum(lloc);
+  if (lane == 0) red[4 + wave] = lloc;
+  __syncthreads();
+  const float L = (red[4] + red[5]) + (red[6] + red[7]);
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
-    float acc = 0.0f;
-    for (int i = 0; i < nparts; ++i) {
-      const float m = p.ws_ml[(row0 + i) * 2];
-      if (m != -INFINITY) acc = fmaf(expf(m - M), p.ws_o[(row0 + i) * p.D + d], acc);
+  if (p.D > 128) {
+    for (int d = tid; d < p.D; d += 256) {
+      float acc = 0.0f;
+      for (int i = 0; i < nparts; ++i) {
+        const float m = ml[i * 2];
+        if (m != -INFINITY) acc = fmaf(expf(m - M), po[(int64_t)i * p.D + d], acc);
+      }
+      OutE::store(o + d, acc * inv);
     }
-    OutE::store(o + d, acc * inv);
+    return;
+  }
+  const int ng = 256 / p.D;
+  const int grp = tid / p.D, d = tid % p.D;
+  float acc = 0.0f;
+  if (grp < ng) {
+#pragma unroll 4
+    for (int i = grp; i < nparts; i += ng) {
+      const float m = ml[i * 2];
+      const float w = m != -INFINITY ? expf(m - M) : 0.0f;
+      acc = fmaf(w, po[(int64_t)i * p.D + d], acc);
+    }
+  }
+  part_acc[tid] = acc;
+  __syncthreads();
+  if (tid < p.D) {
+    float s = 0.0f;
+    for (int g = 0; g < ng; ++g) s += part_acc[g * p.D + tid];
+    OutE::store(o + tid, s * inv);
   }
 }
 
@@ -220,7 +257,7 @@ int32_t launch_decode_generic(const DecodeParams& p, int q_dt, int kv_dt, hipStr
 
 int32_t launch_decode_reduce(const DecodeParams& p, int q_dt, hipStream_t stream) {
   const dim3 grid(p.Hq, p.B);
-  const int threads = p.D <= 64 ? 64 : (p.D <= 128 ? 128 : 256);
+  const int threads = 256;
   ProfileScope prof("cf_decode_reduce", stream);
   switch (q_dt) {
     case kF32: hipLaunchKernelGGL((decode_reduce_kernel<kF32>), grid, dim3(threads), 0, stream, p); break;

@@ -172,14 +172,25 @@ def test_fp8_cache_requires_scales_and_workspace_is_checked():
 def test_workspace_size_formula():
     n = ctypes.c_uint64()
     lib = _abi.lib()
+    def generic_bytes(batch, hq, d, parts):
+        if parts <= 1:
+            return 0
+        rows = batch * hq * parts
+        return ((rows * d * 4 + 255) // 256) * 256 + rows * 8
+
     # block size 8: the generic path only -> partition partials
-    assert lib.cf_paged_decode_workspace_bytes(64, 32, 8, 128, 32, 8, 512, ctypes.byref(n)) == 0
-    assert n.value == 0  # a single partition needs no workspace
     assert lib.cf_paged_decode_workspace_bytes(64, 32, 8, 128, 1024, 8, 512, ctypes.byref(n)) == 0
-    parts = 1024 * 8 // 512
-    rows = 64 * 32 * parts
-    o = rows * 128 * 4
-    assert n.value == ((o + 255) // 256) * 256 + rows * 8
+    # 64 x 8 x 16 partitions of 512 tokens already fill the GPU: the caller's length stands
+    assert n.value == generic_bytes(64, 32, 128, 1024 * 8 // 512)
+    assert lib.cf_paged_decode_workspace_bytes(64, 32, 8, 128, 32, 8, 512, ctypes.byref(n)) == 0
+    # 256 tokens: one partition of 512 would give 512 workgroups, so the generic path
+    # halves the partition (512 -> 256 -> 128) until 64 x 8 x 2 = 1024 workgroups
+    assert n.value == generic_bytes(64, 32, 128, 2)
+    assert lib.cf_paged_decode_workspace_bytes(1, 8, 8, 128, 2, 8, 512, ctypes.byref(n)) == 0
+    assert n.value == 0  # 16 tokens: one partition at the 32-token floor, no workspace
+    # small batch (the opt-125m shape): 4 x 12 heads, 512 tokens -> partitions of 32 tokens
+    assert lib.cf_paged_decode_workspace_bytes(4, 12, 12, 64, 32, 8, 512, ctypes.byref(n)) == 0
+    assert n.value == generic_bytes(4, 12, 64, 256 // 32)
     # block size 16: at least the MFMA path's per-wave slots
     assert lib.cf_paged_decode_workspace_bytes(64, 32, 8, 128, 32, 16, 512, ctypes.byref(n)) == 0
     assert n.value > 0 and n.value % 8 == 0
