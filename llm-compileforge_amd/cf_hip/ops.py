@@ -427,6 +427,48 @@ def copy_blocks(cache: torch.Tensor, pairs: torch.Tensor) -> None:
     check(rc, "cf_copy_blocks")
 
 
+# ---- side-by-side work on one device ------------------------------------------
+# Decode attention is bound by HBM and chunked prefill by the MFMA pipes.  The
+# decode kernel keeps one workgroup per CU (166 VGPRs a wave), which leaves
+# register room for one prefill workgroup (250 VGPRs a wave) beside it on
+# every CU, so the two kernels overlap when they sit on two streams.
+_SIDE: dict[int, tuple[torch.cuda.Stream, torch.cuda.Event, torch.cuda.Event]] = {}
+
+
+def _side_stream(device: torch.device) -> tuple[torch.cuda.Stream, torch.cuda.Event, torch.cuda.Event]:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    entry = _SIDE.get(idx)
+    if entry is None:
+        # default priority, like every stream of this library
+        entry = (torch.cuda.Stream(device=torch.device("cuda", idx)), torch.cuda.Event(), torch.cuda.Event())
+        _SIDE[idx] = entry
+    return entry
+
+
+def run_concurrent(main, side, device: torch.device, keep: tuple[torch.Tensor, ...] = ()) -> None:
+    """Runs `main()` on the current stream and `side()` on a side stream of
+    `device`, so their kernels can execute at the same time.
+
+    Ordering: `side` starts after the work already queued on the current
+    stream; work queued on the current stream after this call starts after
+    both.  `keep` lists the tensors `side` uses that the caller may free
+    afterwards (the caching allocator then waits for the side stream before
+    reusing their memory).  Both callables enqueue work only: no host
+    synchronization happens here.
+    """
+    cur = torch.cuda.current_stream(device)
+    stream, forked, joined = _side_stream(device)
+    forked.record(cur)
+    stream.wait_event(forked)
+    main()
+    with torch.cuda.stream(stream):
+        side()
+    for t in keep:
+        t.record_stream(stream)
+    joined.record(stream)
+    cur.wait_event(joined)
+
+
 class KernelTimer:
     """Sums device time of this library's kernel launches (HIP events)."""
 
@@ -461,6 +503,7 @@ __all__ = [
     "prefill_chunk",
     "prefill_workspace_bytes",
     "new_workspace",
+    "run_concurrent",
     "fp8_amax_scale",
     "fp8_dequantize",
     "fp8_quantize",

@@ -207,6 +207,36 @@ def test_c5_full_step(gpu):
     assert_close(got, ref, torch.bfloat16, "c5 sampled rows")
 
 
+def test_c5_step_two_streams(gpu):
+    """Decode and prefill side by side (ops.run_concurrent) give the same
+    bits as one after another, on every call of a repeated step whose
+    outputs the caller's stream then reads."""
+    print("[case] c5 step, decode || prefill on two streams", flush=True)
+    case = workloads.make_mixed_case(device=gpu, seed=0)
+    t = workloads.materialize_mixed(case)
+    _write_new_rows(case, t)
+    plan = ops.DecodePlan(t["q_decode"], t["k_cache"], t["v_cache"], t["decode_tables"], t["decode_lens"],
+                          case.scale, 16, t["k_scale"], t["v_scale"])
+    dec_ref = plan.run().clone()
+    pre_ref = _prefill(case, t).clone()
+    out = torch.empty_like(pre_ref)
+
+    def prefill():
+        chunked_prefill_attention(t["q_prefill"], t["k_cache"], t["v_cache"], t["prefill_tables"],
+                                  t["prefill_lens"], t["q_start"], 16, case.scale, k_scale=t["k_scale"],
+                                  v_scale=t["v_scale"], out=out)
+
+    for i in range(3):
+        plan.out.zero_()
+        out.zero_()
+        ops.run_concurrent(plan.run, prefill, gpu, keep=(out,))
+        # read on the caller's stream: ordered after both
+        same_dec = torch.equal(plan.out, dec_ref)
+        same_pre = torch.equal(out, pre_ref)
+        torch.cuda.synchronize()
+        assert same_dec and same_pre, f"call {i}: decode equal {same_dec}, prefill equal {same_pre}"
+
+
 def test_hal_op(gpu):
     from python_runtime.hal.hip_backend import HipBackend
 
