@@ -132,22 +132,25 @@ def bench_mixed(args) -> dict:
     torch.cuda.synchronize()
     log(f"c5: {alg['decode_tokens']} decodes, {alg['prefill_tokens']} chunk rows; decode bytes "
         f"{alg['decode_bytes'] / 1e9:.2f} GB, prefill {alg['prefill_flops'] / 1e9:.1f} GFLOP")
+    one = args.one_stream
     for i in range(args.warmup):
-        steps_fns[i % len(steps_fns)]()
+        steps_fns[i % len(steps_fns)](serial=one)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        steps_fns[i % len(steps_fns)]()
+        steps_fns[i % len(steps_fns)](serial=one)
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
     # The same steps on one stream (kernels one after another), for the
     # per-kernel durations below and as the no-overlap reference.
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        steps_fns[i % len(steps_fns)](serial=True)
-    torch.cuda.synchronize()
-    ms_serial = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_serial = ms_step
+    if not one:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            steps_fns[i % len(steps_fns)](serial=True)
+        torch.cuda.synchronize()
+        ms_serial = (time.perf_counter() - t0) * 1e3 / args.steps
     with ops.KernelTimer() as timer:
         for i in range(args.steps):
             steps_fns[i % len(steps_fns)](serial=True)
@@ -183,7 +186,7 @@ def bench_mixed(args) -> dict:
                    "block_size": case.block_size, "kv_layout": args.layout, "cache_pools_rotated": args.pools,
                    "parallelism": "single GPU"},
         "kernel_us": us,
-        "overlap": {"decode_prefill_streams": 2, "ms_per_step_one_stream": ms_serial,
+        "overlap": {"decode_prefill_streams": 1 if one else 2, "ms_per_step_one_stream": ms_serial,
                     "note": "kernel_us are one-stream durations; value is the two-stream step"},
         "algorithmic": alg,
         "roofline": {"bound": "hbm", "kernel": "cf_decode_mfma", "achieved": dec_gbs, "peak": HBM_PEAK_GBS,
@@ -338,6 +341,8 @@ def main() -> None:
     ap.add_argument("--cpu-sample", type=int, default=8)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--one-stream", action="store_true",
+                    help="c5_mixed: decode and prefill one after another only (per-kernel profiles)")
     ap.add_argument("--no-shared-prefix", action="store_true",
                     help="do not pass the shared-prefix statement (every sequence reads its whole table)")
     args = ap.parse_args()
