@@ -194,6 +194,33 @@ def test_long_single_sequence_split_over_many_waves(gpu, kv_dtype):
     assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, "long sequence")
 
 
+@pytest.mark.parametrize("kv_dtype,bs,d", [(torch.float32, 16, 64), (torch.float32, 16, 256), (torch.bfloat16, 8, 80)])
+def test_generic_path_many_partitions(gpu, kv_dtype, bs, d):
+    """The generic (VALU) path on a small batch: the partition length shrinks
+    to 32 tokens, so a 20000-token sequence leaves 625 partials per query head
+    for the merge (more than its 256 threads, in several groups per channel)."""
+    print(f"[case] generic many partitions kv={kv_dtype} bs={bs} d={d}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(31)
+    lens = [20000, 5]
+    hq, hkv = 4, 2
+    nb = sum((n + bs - 1) // bs for n in lens) + 2
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(4)).tolist()
+    tables, pos = [], 0
+    for n in lens:
+        k = (n + bs - 1) // bs
+        tables.append(perm[pos:pos + k])
+        pos += k
+    q_dtype = torch.float32 if kv_dtype == torch.float32 else torch.bfloat16
+    q = torch.randn(len(lens), hq, d, generator=g, device=gpu).to(q_dtype)
+    ksrc = torch.randn(nb, bs, hkv, d, generator=g, device=gpu).to(q_dtype)
+    vsrc = torch.randn(nb, bs, hkv, d, generator=g, device=gpu).to(q_dtype)
+    case = workloads.DecodeCase("generic", q, ksrc, vsrc, tables, lens, bs, 1 / math.sqrt(d), kv_dtype)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    out = _run(case, kc, vc, ks, vs, gpu)
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    assert_close(out.float().cpu().numpy(), ref, q_dtype, f"generic {kv_dtype}/{bs}/{d}")
+
+
 def test_repeated_calls_share_a_workspace(gpu):
     """Repeated calls on one workspace give bit-identical outputs, also after
     a call with another batch shape in between."""
