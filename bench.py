@@ -84,12 +84,17 @@ def cpu_baseline(case, kc, vc, ks, vs, sample: int, budget_s: float) -> dict:
     }
 
 
-def load_traffic(config: str) -> float | None:
+def load_traffic(config: str, kernel: str | None = None) -> float | None:
+    """Calibrated HBM bytes per launch (FETCH_SIZE / WRITE_SIZE counter
+    runs, profiles/traffic_<config>.json) of the config's main kernel, or of
+    `kernel` where the file lists several."""
     path = ROOT / "profiles" / f"traffic_{config}.json"
     if path.exists():
         try:
-            return float(json.loads(path.read_text())["hbm_bytes_per_launch"])
-        except (KeyError, ValueError):
+            data = json.loads(path.read_text())
+            entry = data["kernels"][kernel] if kernel is not None else data
+            return float(entry["hbm_bytes_per_launch"])
+        except (KeyError, ValueError, TypeError):
             return None
     return None
 
@@ -190,10 +195,11 @@ def bench_mixed(args) -> dict:
                     "note": "kernel_us are one-stream durations; value is the two-stream step"},
         "algorithmic": alg,
         "roofline": {"bound": "hbm", "kernel": "cf_decode_mfma", "achieved": dec_gbs, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": dec_gbs / HBM_PEAK_GBS, "traffic": None},
+                     "unit": "GB/s", "frac": dec_gbs / HBM_PEAK_GBS,
+                     "traffic": load_traffic(args.config, "cf_decode_mfma")},
         "roofline_prefill": {"bound": "mfma", "kernel": "cf_prefill_mfma", "achieved": pre_tf,
                              "peak": BF16_MFMA_PEAK_TFS, "unit": "TFLOP/s", "frac": pre_tf / BF16_MFMA_PEAK_TFS,
-                             "traffic": None},
+                             "traffic": load_traffic(args.config, "cf_prefill_mfma")},
     }
 
 
