@@ -226,6 +226,9 @@ int32_t cf_fp8_dequantize(const CfTensor* q, const CfTensor* scales,
  *   v_cache
  *   k_scale,      [Hkv] or [1]      f32
  *   v_scale
+ * Slots must be distinct: rows that repeat a slot race, and which one lands
+ * is not defined (the reference's sequential loop keeps the last; the
+ * engine's CacheManager drops the earlier repeats before it calls here).
  * The caller must not target a block that other sequences share. */
 int32_t cf_kv_write_fp8(const CfTensor* k_new, const CfTensor* v_new,
                         const CfTensor* slot_mapping, CfTensor* k_cache,
@@ -243,6 +246,8 @@ int32_t cf_kv_write_fp8(const CfTensor* k_new, const CfTensor* v_new,
  *   slot_mapping  [T]              i32 | i64
  *   cache         [NB, bs, H, D]   f32 | f16 | bf16 | e4m3fn, any strides
  *   scale         [H] or [1] f32   (e4m3fn caches; NULL otherwise)
+ * Slots must be distinct (repeats race; CacheManager keeps the last of
+ * each before calling).
  * The caller must not target a slot that another sequence still reads. */
 int32_t cf_paged_write(const CfTensor* x_new, const CfTensor* slot_mapping,
                        CfTensor* cache, const CfTensor* scale, void* stream);

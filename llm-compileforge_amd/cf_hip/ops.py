@@ -327,7 +327,9 @@ def kv_write_fp8(
     k_scale: torch.Tensor,
     v_scale: torch.Tensor,
 ) -> None:
-    """Quantizes new K/V rows [T, Hkv, D] into paged e4m3fn caches at slot_mapping[T]."""
+    """Quantizes new K/V rows [T, Hkv, D] into paged e4m3fn caches at
+    slot_mapping[T].  Slots must be distinct (rows repeating a slot race);
+    slots outside the cache are skipped."""
     for name, t in (("k_new", k_new), ("v_new", v_new), ("slot_mapping", slot_mapping), ("k_cache", k_cache),
                     ("v_cache", v_cache), ("k_scale", k_scale), ("v_scale", v_scale)):
         _require_device(name, t)
@@ -344,7 +346,8 @@ def paged_write(
 ) -> None:
     """Writes rows x_new [T, H, D] into a paged cache [NB, bs, H, D] (any
     layout) at slots block * bs + offset; e4m3fn caches quantize with the
-    per-head `scale` [H] (or one scale).  Slots outside the cache are skipped."""
+    per-head `scale` [H] (or one scale).  Slots outside the cache are
+    skipped; slots must be distinct (rows repeating a slot race)."""
     for name, t in (("x_new", x_new), ("slot_mapping", slot_mapping), ("cache", cache)):
         _require_device(name, t)
     dev = _same_device(x_new, slot_mapping, cache)
