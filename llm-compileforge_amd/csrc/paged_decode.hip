@@ -10,6 +10,11 @@
 // partition is PT consecutive tokens.  With more than one partition per
 // sequence the workgroup writes (m, l, o) partials, merged by
 // decode_reduce; with a single partition it writes the output directly.
+// Scores: 16 lanes per token, each taking every 16th channel (consecutive
+// lanes read consecutive channels of a K row), summed across the 16 lanes.
+// P.V: the G * D outputs are spread over the 256 threads and, when there are
+// fewer outputs than threads, the partition's tokens are split between
+// thread groups whose sums meet in LDS.
 #include "cf_device.hpp"
 #include "cf_host.hpp"
 #include "decode_params.hpp"
@@ -51,6 +56,8 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
   float* sq = smem;                           // [G][D]
   float* sc = sq + G * D;                     // [G][PT]
   int* sblk = (int*)(sc + G * PT);            // [PT / bs]
+  float* sml = (float*)(sblk + ((PT / bs + 1) & ~1));  // [G][2]
+  float* sacc = sml + 2 * G;                  // [256] P.V partial sums
 
   using QE = Elem<QT>;
   using KE = Elem<KT>;
@@ -69,29 +76,51 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
   const float vs = p.v_scale ? p.v_scale[h * p.vs_s] : 1.0f;
   const float qk_scale = p.scale * ks;
 
-  // scores
+  // scores: token i on the 16 lanes of slot i % 16, channels sub, sub + 16, ...
+  constexpr int kChunk = 8;  // channels per lane held in registers at once
   const typename KE::T* kbase = (const typename KE::T*)p.k;
-  for (int i = tid; i < count; i += kGenericThreads) {
+  const int sub = tid & 15, slot = tid >> 4;
+  for (int i0 = 0; i0 < count; i0 += kGenericThreads / 16) {
+    const int i = i0 + slot;
+    const bool tok_ok = i < count;
     const int tok = start + i;
-    const int64_t blk = sblk[i / bs];
-    if ((uint32_t)blk >= (uint32_t)p.NB) {
-      for (int g = 0; g < G; ++g) sc[g * PT + i] = -INFINITY;
-      continue;
-    }
+    const int64_t blk = tok_ok ? sblk[i / bs] : -1;
+    const bool blk_ok = (uint64_t)blk < (uint64_t)p.NB;
     const typename KE::T* krow =
-        kbase + blk * p.k_s[0] + (int64_t)(tok % bs) * p.k_s[1] + (int64_t)h * p.k_s[2];
-    for (int g = 0; g < G; ++g) {
-      float acc = 0.0f;
-      const float* qg = sq + g * D;
-      for (int d = 0; d < D; ++d) acc = fmaf(qg[d], KE::load(krow + (int64_t)d * p.k_s[3]), acc);
-      sc[g * PT + i] = acc * qk_scale;
+        kbase + (blk_ok ? blk : 0) * p.k_s[0] + (int64_t)(tok % bs) * p.k_s[1] + (int64_t)h * p.k_s[2];
+    for (int d0 = 0; d0 < D; d0 += 16 * kChunk) {
+      float kv[kChunk];
+#pragma unroll
+      for (int c = 0; c < kChunk; ++c) {
+        const int d = d0 + sub + 16 * c;
+        kv[c] = (blk_ok && d < D) ? KE::load(krow + (int64_t)d * p.k_s[3]) : 0.0f;
+      }
+      for (int g = 0; g < G; ++g) {
+        const float* qg = sq + g * D;
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kChunk; ++c) {
+          const int d = d0 + sub + 16 * c;
+          if (d < D) acc = fmaf(qg[d], kv[c], acc);
+        }
+        // sum over the token's 16 lanes (aligned groups of 16)
+        acc += __shfl_xor(acc, 8, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 1, 64);
+        if (sub == 0 && tok_ok) {
+          const float prev = d0 == 0 ? 0.0f : sc[g * PT + i];
+          sc[g * PT + i] = prev + acc;
+        }
+      }
     }
+    if (sub == 0 && tok_ok)
+      for (int g = 0; g < G; ++g) sc[g * PT + i] = blk_ok ? sc[g * PT + i] * qk_scale : -INFINITY;
   }
   __syncthreads();
 
   // softmax statistics per query head: one wave per head
   const int wave = tid / 64, lane = tid % 64;
-  float* sml = (float*)(sblk + ((PT / bs + 1) & ~1));  // [G][2]
   for (int g = wave; g < G; g += kGenericThreads / 64) {
     float m = -INFINITY;
     for (int i = lane; i < count; i += 64) m = fmaxf(m, sc[g * PT + i]);
@@ -110,18 +139,35 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
   }
   __syncthreads();
 
-  // p . v
+  // p . v: output (g, d) = sum over tokens; with GD < 256 outputs the tokens
+  // are dealt round-robin to ng = 256 / GD thread groups
   const typename KE::T* vbase = (const typename KE::T*)p.v;
-  for (int i = tid; i < G * D; i += kGenericThreads) {
-    const int g = i / D, d = i % D;
+  const int GD = G * D;
+  const int ng = GD < kGenericThreads ? kGenericThreads / GD : 1;
+  for (int o0 = 0; o0 < GD; o0 += kGenericThreads) {
+    const int grp = ng > 1 ? tid / GD : 0;
+    const int o = ng > 1 ? tid % GD : o0 + tid;
+    const bool active = grp < ng && o < GD;
+    const int g = active ? o / D : 0, d = active ? o % D : 0;
     float acc = 0.0f;
-    for (int t = 0; t < count; ++t) {
-      const int tok = start + t;
-      const int64_t blk = sblk[t / bs];
-      if ((uint32_t)blk >= (uint32_t)p.NB) continue;
-      const typename KE::T* vrow =
-          vbase + blk * p.v_s[0] + (int64_t)(tok % bs) * p.v_s[1] + (int64_t)h * p.v_s[2];
-      acc = fmaf(sc[g * PT + t], KE::load(vrow + (int64_t)d * p.v_s[3]), acc);
+    if (active) {
+      for (int t = grp; t < count; t += ng) {
+        const int tok = start + t;
+        const int64_t blk = sblk[t / bs];
+        if ((uint64_t)blk >= (uint64_t)p.NB) continue;
+        const typename KE::T* vrow =
+            vbase + blk * p.v_s[0] + (int64_t)(tok % bs) * p.v_s[1] + (int64_t)h * p.v_s[2];
+        acc = fmaf(sc[g * PT + t], KE::load(vrow + (int64_t)d * p.v_s[3]), acc);
+      }
+    }
+    if (ng > 1) {
+      sacc[tid] = acc;
+      __syncthreads();
+      if (tid >= GD) break;  // GD < 256: one pass, the first GD threads finish it
+      acc = 0.0f;
+      for (int k = 0; k < ng; ++k) acc += sacc[k * GD + tid];
+    } else if (!active) {
+      continue;
     }
     acc *= vs;
     const int hq = h * G + g;
@@ -214,7 +260,7 @@ template <int QT, int KT>
 int32_t launch_generic_t(const DecodeParams& p, hipStream_t stream) {
   const dim3 grid(p.max_parts, p.Hkv, p.B);
   const size_t sml_off = (size_t)p.G * p.D + (size_t)p.G * p.PT + (size_t)(((p.PT / p.bs + 1) & ~1));
-  const size_t lds = (sml_off + 2 * (size_t)p.G) * 4;
+  const size_t lds = (sml_off + 2 * (size_t)p.G + kGenericThreads) * 4;
   if (lds > 64 * 1024) {
     set_error("generic decode needs %zu bytes of LDS (G=%d, D=%d, partition=%d); use a smaller partition",
               lds, p.G, p.D, p.PT);
