@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 from pathlib import Path
 from typing import Any
 
@@ -95,26 +96,25 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise ValueError(f"dtype {dtype} has no cf_hip code") from None
 
 
+# CfTensor as bytes: SFATensor {device, rank, elem_size (i32), pad, union
+# at 16: allocated, aligned (pointers), offset, sizes[r], strides[r] (i64)},
+# then dtype, reserved (i32) at 104.  One pack per descriptor (the
+# structures below give the same layout; tests/test_abi.py compares them).
+_PACK = {r: struct.Struct(f"<iii4xQQq{r}q{r}q{(4 - r) * 16}xii") for r in (1, 2, 3, 4)}
+
+
 def descriptor(t: torch.Tensor) -> CfTensor:
     """Builds a CfTensor over `t` (no copy; `t` must outlive the call)."""
     rank = t.dim()
     if not 1 <= rank <= 4:
         raise ValueError(f"cf_hip descriptors have rank 1..4, got a rank-{rank} tensor")
-    d = CfTensor()
-    d.dtype = dtype_code(t.dtype)
-    d.t.device = SFA_ROCM if t.is_cuda else SFA_CPU
-    d.t.rank = rank
-    d.t.elem_size = t.element_size()
-    raw = getattr(d.t, f"r{rank}")
+    esize = t.element_size()
+    off = t.storage_offset()
     # The storage base plus the element offset, like a memref descriptor.
-    base = t.data_ptr() - t.storage_offset() * t.element_size()
-    raw.allocated = base
-    raw.aligned = base
-    raw.offset = t.storage_offset()
-    for i in range(rank):
-        raw.sizes[i] = t.shape[i]
-        raw.strides[i] = t.stride(i)
-    return d
+    base = t.data_ptr() - off * esize
+    return CfTensor.from_buffer_copy(_PACK[rank].pack(
+        SFA_ROCM if t.is_cuda else SFA_CPU, rank, esize, base, base, off, *t.shape, *t.stride(),
+        dtype_code(t.dtype), 0))
 
 
 def _lib_path() -> Path:
@@ -248,5 +248,11 @@ def ref(d: CfTensor | None) -> Any:
     return ctypes.byref(d) if d is not None else None
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """The current stream of `device` as a hipStream_t value."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream

@@ -5,6 +5,7 @@
  * unboxing block ids one object at a time).
  *
  * pack(block_tables, seq_lens, block_size, num_blocks, out, width) -> mb
+ * width(block_tables) -> the longest table's length
  *
  *   block_tables: dict request id -> sequence of block ids (insertion order)
  *   seq_lens:     dict request id -> length; a missing id means
@@ -140,8 +141,26 @@ done:
   return result;
 }
 
+/* width(block_tables) -> the longest table's length (0 for no tables). */
+static PyObject* width(PyObject* self, PyObject* arg) {
+  (void)self;
+  if (!PyDict_Check(arg)) {
+    PyErr_SetString(PyExc_TypeError, "block_tables must be a dict");
+    return NULL;
+  }
+  Py_ssize_t pos = 0, w = 0;
+  PyObject *key, *val;
+  while (PyDict_Next(arg, &pos, &key, &val)) {
+    const Py_ssize_t n = PyObject_Length(val);
+    if (n < 0) return NULL;
+    if (n > w) w = n;
+  }
+  return PyLong_FromSsize_t(w);
+}
+
 static PyMethodDef methods[] = {
     {"pack", pack, METH_VARARGS, "pack(block_tables, seq_lens, block_size, num_blocks, out, width) -> mb"},
+    {"width", width, METH_O, "width(block_tables) -> longest table length"},
     {NULL, NULL, 0, NULL},
 };
 

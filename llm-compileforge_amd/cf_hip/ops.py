@@ -7,6 +7,7 @@ path: a CPU tensor or a missing libcf_hip.so raises.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -22,6 +23,16 @@ def _require_device(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
     if not t.is_cuda or torch.version.hip is None:
         raise ValueError(f"{name} must be a ROCm device tensor (got device {t.device})")
+
+
+_SAME = contextlib.nullcontext()
+
+
+def _on(device: torch.device):
+    """Makes `device` current for a library call (a no-op when it is)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _SAME
+    return torch.cuda.device(device)
 
 
 def _same_device(*ts: torch.Tensor) -> torch.device:
@@ -140,7 +151,7 @@ def paged_decode(
         dsh = descriptor(shared_prefix_lens)
     dq, dk, dv = descriptor(q), descriptor(k_cache), descriptor(v_cache)
     dt, dsl, do = descriptor(block_tables), descriptor(seq_lens), descriptor(out)
-    with torch.cuda.device(dev):
+    with _on(dev):
         rc = lib().cf_paged_decode_shared(
             ref(dq), ref(dk), ref(dv), ref(dt), ref(dsl), ref(dsh), ref(ks), ref(vs),
             float(scale), int(block_size), int(partition_tokens), ref(do),
@@ -199,7 +210,7 @@ def prefill_chunk(
     vs = descriptor(v_scale) if v_scale is not None else None
     d = [descriptor(t) for t in (q, k_cache, v_cache, block_tables, seq_lens, q_start)]
     do = descriptor(out)
-    with torch.cuda.device(dev):
+    with _on(dev):
         rc = lib().cf_prefill_chunk_fp8(
             *(ref(x) for x in d), ref(ks), ref(vs), float(scale), int(block_size), ref(do),
             workspace.data_ptr(), need, stream_handle(dev),
@@ -336,7 +347,7 @@ def kv_write_fp8(
     dev = _same_device(k_new, v_new, slot_mapping, k_cache, v_cache, k_scale, v_scale)
     ds = [descriptor(t) for t in (k_new, v_new, slot_mapping, k_cache, v_cache, k_scale.reshape(-1),
                                    v_scale.reshape(-1))]
-    with torch.cuda.device(dev):
+    with _on(dev):
         rc = lib().cf_kv_write_fp8(*(ref(d) for d in ds), stream_handle(dev))
     check(rc, "cf_kv_write_fp8")
 
@@ -356,7 +367,7 @@ def paged_write(
     if scale is not None:
         _require_device("scale", scale)
         dsc = descriptor(scale.reshape(-1))
-    with torch.cuda.device(dev):
+    with _on(dev):
         rc = lib().cf_paged_write(ref(ds[0]), ref(ds[1]), ref(ds[2]), ref(dsc), stream_handle(dev))
     check(rc, "cf_paged_write")
 
@@ -383,7 +394,7 @@ def paged_gather(
         _require_device("scale", scale)
         dsc = descriptor(scale.reshape(-1))
     dc, dt_, do = descriptor(cache), descriptor(block_tables), descriptor(out)
-    with torch.cuda.device(dev):
+    with _on(dev):
         rc = lib().cf_paged_gather(ref(dc), ref(dt_), ref(dsc), ref(do), stream_handle(dev))
     check(rc, "cf_paged_gather")
     return out
@@ -396,7 +407,7 @@ def block_tables_apply(table: torch.Tensor, lens: torch.Tensor, deltas: torch.Te
         _require_device(name, t)
     dev = _same_device(table, lens, deltas)
     dt, dl, dd = descriptor(table), descriptor(lens), descriptor(deltas)
-    with torch.cuda.device(dev):
+    with _on(dev):
         rc = lib().cf_block_tables_apply(ref(dt), ref(dl), ref(dd), stream_handle(dev))
     check(rc, "cf_block_tables_apply")
 
@@ -425,7 +436,7 @@ def copy_blocks(cache: torch.Tensor, pairs: torch.Tensor) -> None:
     dev = _same_device(cache, pairs)
     flat = block_span_view(cache).view(torch.uint8)  # bytes: any element type
     dc, dp = descriptor(flat), descriptor(pairs)
-    with torch.cuda.device(dev):
+    with _on(dev):
         rc = lib().cf_copy_blocks(ref(dc), ref(dp), stream_handle(dev))
     check(rc, "cf_copy_blocks")
 

@@ -74,8 +74,17 @@ def _pack_tables_py(block_tables: dict, seq_lens: dict, block_size: int, nb: int
 
 try:  # the CPython packer next to the ctypes binding (built by csrc/build.py)
     from cf_hip._tablepack import pack as _pack_native
+    from cf_hip._tablepack import width as _width_native
 except ImportError:  # pragma: no cover - exercised when only the HIP library is built
     _pack_native = None
+    _width_native = None
+
+
+def table_width(block_tables: dict) -> int:
+    """The longest block table's length."""
+    if _width_native is not None:
+        return _width_native(block_tables)
+    return max((len(t) for t in block_tables.values()), default=0)
 
 
 def pack_tables(block_tables: dict, seq_lens: dict, block_size: int, nb: int, out: np.ndarray, width: int) -> int:
@@ -220,7 +229,7 @@ def paged_attention(
         return {}
     nb = k_cache.shape[0]
     n_req = len(rids)
-    width = max(len(t) for t in block_tables.values())
+    width = table_width(block_tables)
     host = _staging(q.device, n_req * (width + 2))
     mb = pack_tables(block_tables, seq_lens, block_size, nb, host.numpy(), width)
     dev = host[: n_req * (mb + 2)].to(q.device, non_blocking=True)

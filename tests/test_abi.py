@@ -82,6 +82,24 @@ def test_descriptor_of_a_strided_view():
     assert d.t.r4.aligned + d.t.r4.offset * 4 == view.data_ptr()
 
 
+@pytest.mark.parametrize("rank", [1, 2, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.int32, torch.float8_e4m3fn])
+def test_descriptor_fields_every_rank(rank, dtype):
+    """The packed descriptor reads back field by field through the ctypes
+    structures (the layout of include/cf_hip.h)."""
+    full = torch.zeros(7 * 6 * 5 * 4, dtype=torch.float32).to(dtype).reshape(7, 6, 5, 4)
+    view = full[(slice(1, None, 2),) * rank].reshape(full[(slice(1, None, 2),) * rank].shape)
+    while view.dim() > rank:
+        view = view[0]
+    d = _abi.descriptor(view)
+    raw = getattr(d.t, f"r{rank}")
+    assert (d.t.device, d.t.rank, d.t.elem_size) == (_abi.SFA_CPU, rank, view.element_size())
+    assert d.dtype == _abi.dtype_code(dtype) and d.reserved == 0
+    assert list(raw.sizes) == list(view.shape) and list(raw.strides) == list(view.stride())
+    assert raw.offset == view.storage_offset()
+    assert raw.allocated == raw.aligned == view.data_ptr() - view.storage_offset() * view.element_size()
+
+
 def _call_decode(q, k, v, bt, sl, out, ks=None, vs=None, bs=16, pt=512):
     lib = _abi.lib()
     ds = [_abi.descriptor(t) for t in (q, k, v, bt, sl, out)]

@@ -83,3 +83,13 @@ def test_errors(fn):
         f({"a": []}, {}, 16, 10, buf, 1)
     # an id past the length is never read, so it is not checked
     assert f({"a": [1, 99]}, {"a": 16}, 16, 10, buf, 2) == 1
+
+
+def test_width_matches_python():
+    from cf_hip._tablepack import width
+
+    tables = {"a": [1, 2, 3], "b": [], "c": list(range(40)), "d": (5, 6)}
+    assert width(tables) == max(len(t) for t in tables.values()) == 40
+    assert width({}) == 0
+    with pytest.raises(TypeError):
+        width([[1, 2]])
