@@ -28,6 +28,21 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* An int object's value: one-digit ints (|v| < 2**30, every block id in
+ * practice) are read straight from the object on CPython < 3.12, whose int
+ * layout this relies on; anything else goes through PyLong_AsLongLong. */
+static inline long long id_value(PyObject* o) {
+#if PY_VERSION_HEX < 0x030C0000
+  if (PyLong_CheckExact(o)) {
+    const Py_ssize_t sz = Py_SIZE(o);
+    if (sz == 0) return 0;
+    if (sz == 1) return (long long)((PyLongObject*)o)->ob_digit[0];
+    if (sz == -1) return -(long long)((PyLongObject*)o)->ob_digit[0];
+  }
+#endif
+  return PyLong_AsLongLong(o);
+}
+
 static long long floordiv(long long a, long long b) {
   long long q = a / b;
   if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
@@ -107,7 +122,7 @@ static PyObject* pack(PyObject* self, PyObject* args) {
     PyObject** items = PySequence_Fast_ITEMS(seqs[i]);
     int32_t* row = o + i * mb;
     for (long long j = 0; j < nblk[i]; ++j) {
-      long long bid = PyLong_AsLongLong(items[j]);
+      long long bid = id_value(items[j]);
       if (bid == -1 && PyErr_Occurred()) goto done;
       if (bid < -nb || bid >= nb) {
         PyErr_Format(PyExc_IndexError, "request %R: block id %lld out of range for %lld cache blocks", key, bid, nb);
