@@ -474,13 +474,17 @@ def run_concurrent(main, side, device: torch.device, keep: tuple[torch.Tensor, .
     stream, forked, joined = _side_stream(device)
     forked.record(cur)
     stream.wait_event(forked)
-    main()
-    with torch.cuda.stream(stream):
-        side()
-    for t in keep:
-        t.record_stream(stream)
-    joined.record(stream)
-    cur.wait_event(joined)
+    try:
+        main()
+        with torch.cuda.stream(stream):
+            side()
+        for t in keep:
+            t.record_stream(stream)
+    finally:
+        # also when a callable raised: whatever reached the side stream is
+        # ordered before the caller's later work
+        joined.record(stream)
+        cur.wait_event(joined)
 
 
 class KernelTimer:

@@ -237,6 +237,22 @@ def test_c5_step_two_streams(gpu):
         assert same_dec and same_pre, f"call {i}: decode equal {same_dec}, prefill equal {same_pre}"
 
 
+def test_run_concurrent_orders_work_when_a_callable_raises(gpu):
+    """A side callable that raises after enqueuing work: the error reaches
+    the caller, and the caller's stream still waits for what was enqueued."""
+    x = torch.zeros(1 << 22, device=gpu)
+    big = torch.randn(1 << 22, device=gpu)
+
+    def side():
+        x.copy_(big * 2.0 + 1.0)
+        raise RuntimeError("side failed")
+
+    with pytest.raises(RuntimeError, match="side failed"):
+        ops.run_concurrent(lambda: None, side, gpu)
+    got = (x - (big * 2.0 + 1.0)).abs().max()  # on the caller's stream
+    assert float(got) == 0.0
+
+
 def test_hal_op(gpu):
     from python_runtime.hal.hip_backend import HipBackend
 
