@@ -318,25 +318,25 @@ __device__ __forceinline__ Coord advance(const DecodeParams& p, const Index& ix,
 
 // Q operand columns: column i < ncols is query head (i % G) of KV head h for
 // sequence b + i / G; the rest are zero.
-template <int D>
-__device__ __forceinline__ void load_q(bf16x8_t* qop, const DecodeParams& p, const Coord& c, int li, int lq) {
+template <int QT, int D>
+__device__ __forceinline__ void load_q(QOp<QT>* qop, const DecodeParams& p, const Coord& c, int li, int lq) {
   constexpr int NC = D / 32;
   if (li < c.ncols) {
     const int m = li / p.G, g = li - m * p.G;
     const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(c.b + m) * p.q_sb + (int64_t)(c.h * p.G + g) * p.q_sh +
                            lq * (D / 4);
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) qop[cc] = as_bf16x8(*(const uint4*)(qrow + 8 * cc));
+    for (int cc = 0; cc < NC; ++cc) qop[cc] = as_qop<QT>(*(const uint4*)(qrow + 8 * cc));
   } else {
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) qop[cc] = as_bf16x8(make_uint4(0, 0, 0, 0));
+    for (int cc = 0; cc < NC; ++cc) qop[cc] = as_qop<QT>(make_uint4(0, 0, 0, 0));
   }
 }
 
 // Writes out a finished run (normalized output, record or wave-slot
 // partial) and, from the wave holding the run's first tile, the merge
 // descriptors of the sequences it covers.
-template <bool PL, int D>
+template <int QT, bool PL, int D>
 __device__ __forceinline__ void flush_run(const DecodeParams& p, const Index& ix, const Plan* pl, const Coord& c,
                                           const f32x4_t* o, float m, float l, int run_j0, bool first_run,
                                           int64_t tau, int64_t chunk, int w, int lane) {
@@ -382,8 +382,8 @@ __device__ __forceinline__ void flush_run(const DecodeParams& p, const Index& ix
 #pragma unroll
     for (int t = 0; t < NV; ++t) {
       uint2 packed;
-      packed.x = (uint32_t)bf16_bits_from_f32(o[t][0] * inv) | ((uint32_t)bf16_bits_from_f32(o[t][1] * inv) << 16);
-      packed.y = (uint32_t)bf16_bits_from_f32(o[t][2] * inv) | ((uint32_t)bf16_bits_from_f32(o[t][3] * inv) << 16);
+      packed.x = (uint32_t)out_bits<QT>(o[t][0] * inv) | ((uint32_t)out_bits<QT>(o[t][1] * inv) << 16);
+      packed.y = (uint32_t)out_bits<QT>(o[t][2] * inv) | ((uint32_t)out_bits<QT>(o[t][3] * inv) << 16);
       *(uint2*)(orow + 16 * t) = packed;
     }
     return;
@@ -407,7 +407,7 @@ __device__ __forceinline__ void flush_run(const DecodeParams& p, const Index& ix
   }
 }
 
-template <int KT, int D, bool PL>
+template <int QT, int KT, int D, bool PL>
 __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, const int32_t* __restrict__ tables,
                                                             const int32_t* __restrict__ lens,
                                                             const float* __restrict__ kscale,
@@ -486,8 +486,8 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   TileRegs<KT, D> r0, r1;
   load_tile<KT, D>(r0, kv, c0.blkA, c0.blkB, li, lq, c0.h);
 
-  bf16x8_t qop[NC];
-  load_q<D>(qop, p, c0, li, lq);
+  QOp<QT> qop[NC];
+  load_q<QT, D>(qop, p, c0, li, lq);
   float m = -INFINITY, l = 0.0f;
   f32x4_t o[NV];
 #pragma unroll
@@ -510,8 +510,8 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     f32x4_t s1 = {0.0f, 0.0f, 0.0f, 0.0f}, s2 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_operand<KT>(r0.k1, c), qop[c], s1, 0, 0, 0);
-      s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_operand<KT>(r0.k2, c), qop[c], s2, 0, 0, 0);
+      s1 = mfma16(k_operand_q<QT, KT>(r0.k1, c), qop[c], s1);
+      s2 = mfma16(k_operand_q<QT, KT>(r0.k2, c), qop[c], s2);
     }
     // lane (li, lq): s1[v] -> token 8lq + v, s2[v] -> token 8lq + 4 + v, column li
     float sc[8];
@@ -563,14 +563,19 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     l += psum;
 
     // ---- O^T += V^T P^T --------------------------------------------------
-    if constexpr (KT == kE4M3) {
-      // e4m3 V converts exactly to fp16; P in fp16 (p <= 256) keeps 11 bits.
+    if constexpr (KT == kE4M3 || KT == kF16) {
+      // e4m3 V converts exactly to fp16 (fp16 V is used as is); P in fp16
+      // (p <= 256) keeps 11 bits.
       f16x8_t pop;
 #pragma unroll
       for (int v = 0; v < 8; ++v) pop[v] = (_Float16)pr[v];
 #pragma unroll
-      for (int t = 0; t < NV; ++t)
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(e4m3x8_to_f16(r0.v[t].x, r0.v[t].y), pop, o[t], 0, 0, 0);
+      for (int t = 0; t < NV; ++t) {
+        f16x8_t vop;
+        if constexpr (KT == kE4M3) vop = e4m3x8_to_f16(r0.v[t].x, r0.v[t].y);
+        else vop = __builtin_bit_cast(f16x8_t, r0.v[t]);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, o[t], 0, 0, 0);
+      }
     } else {
       // bf16 V: P = P_hi + P_lo in bf16 (two MFMAs) keeps ~16 bits.
       bf16x8_t pop, plo;
@@ -591,7 +596,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     // ---- end of a run -----------------------------------------------------
     const bool run_ends = !has1 || c1.b != c0.b || c1.h != c0.h || c1.kind != c0.kind;
     if (run_ends) {
-      flush_run<PL, D>(p, ix, pl, c0, o, m, l, run_j0, first_run, tau, chunk, w, lane);
+      flush_run<QT, PL, D>(p, ix, pl, c0, o, m, l, run_j0, first_run, tau, chunk, w, lane);
       first_run = false;
     }
     if (!has1) break;
@@ -602,7 +607,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     r0 = r1;
     ++tau;
     if (run_ends) {
-      load_q<D>(qop, p, c0, li, lq);
+      load_q<QT, D>(qop, p, c0, li, lq);
       m = -INFINITY;
       l = 0.0f;
 #pragma unroll
@@ -626,7 +631,7 @@ __device__ __forceinline__ int64_t part_row(int2 d, int k) {
 // decode kernel did not write whole: its own run's and its group's prefix
 // run's, each a record or the wave slots of a split run.  One wave per
 // (h, b); partial rows hold the G heads of h in consecutive rows.
-template <int D, int G>
+template <int QT, int D, int G>
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
   constexpr int E = G * D / 64;  // output elements per lane
   __shared__ float wgt[64][G];
@@ -697,7 +702,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
           a += w * ov[k][i];
         }
       }
-      out[(int64_t)(h * G + g) * p.o_sh + d] = bf16_bits_from_f32(lg > 0.0f ? a / lg : 0.0f);
+      out[(int64_t)(h * G + g) * p.o_sh + d] = out_bits<QT>(lg > 0.0f ? a / lg : 0.0f);
     }
     return;
   }
@@ -766,7 +771,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
   for (int i = 0; i < E; ++i) {
     const int idx = lane + 64 * i;
     const int g = idx / D, d = idx % D;
-    out[(int64_t)(h * G + g) * p.o_sh + d] = bf16_bits_from_f32(acc[i] * inv_l[g]);
+    out[(int64_t)(h * G + g) * p.o_sh + d] = out_bits<QT>(acc[i] * inv_l[g]);
   }
 }
 
@@ -789,13 +794,13 @@ int cu_count() {
 // Llama-3-8B shape).  The workspace holds slots for this many waves.
 constexpr int kStreamBlocksPerCU = 1;
 
-template <int KT, int D, bool PL>
+template <int QT, int KT, int D, bool PL>
 int blocks_per_cu() {
   static int cached = 0;
   if (cached == 0) {
     int n = 0;
     const size_t lds = PL ? sizeof(Plan) : 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<KT, D, PL>, 256, lds) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<QT, KT, D, PL>, 256, lds) != hipSuccess ||
         n < 1)
       n = 1;
     cached = n < kStreamBlocksPerCU ? n : kStreamBlocksPerCU;
@@ -803,29 +808,29 @@ int blocks_per_cu() {
   return cached;
 }
 
-template <int KT, int D, bool PL>
+template <int QT, int KT, int D, bool PL>
 int32_t launch_stream_t(const DecodeParams& p, hipStream_t stream) {
-  const int blocks = cu_count() * blocks_per_cu<KT, D, PL>();
+  const int blocks = cu_count() * blocks_per_cu<QT, KT, D, PL>();
   ProfileScope prof("cf_decode_mfma", stream);
-  hipLaunchKernelGGL((decode_stream_kernel<KT, D, PL>), dim3(blocks), dim3(256), PL ? sizeof(Plan) : 0, stream, p,
+  hipLaunchKernelGGL((decode_stream_kernel<QT, KT, D, PL>), dim3(blocks), dim3(256), PL ? sizeof(Plan) : 0, stream, p,
                      p.tables, p.seq_lens, p.k_scale, p.v_scale, PL ? p.shared : nullptr);
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
 }
 
-template <int KT, int D>
+template <int QT, int KT, int D>
 int32_t launch_t(const DecodeParams& p, hipStream_t stream) {
-  const int32_t rc = p.B <= kPlanMaxB ? launch_stream_t<KT, D, true>(p, stream)
-                                      : launch_stream_t<KT, D, false>(p, stream);
+  const int32_t rc = p.B <= kPlanMaxB ? launch_stream_t<QT, KT, D, true>(p, stream)
+                                      : launch_stream_t<QT, KT, D, false>(p, stream);
   if (rc) return rc;
   const dim3 grid(p.Hkv, p.B);
   ProfileScope prof("cf_decode_merge", stream);
   switch (p.G) {
-    case 1: hipLaunchKernelGGL((decode_merge_kernel<D, 1>), grid, dim3(64), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((decode_merge_kernel<D, 2>), grid, dim3(64), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((decode_merge_kernel<D, 4>), grid, dim3(64), 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((decode_merge_kernel<D, 8>), grid, dim3(64), 0, stream, p); break;
-    case 16: hipLaunchKernelGGL((decode_merge_kernel<D, 16>), grid, dim3(64), 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 1>), grid, dim3(64), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 2>), grid, dim3(64), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 4>), grid, dim3(64), 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 8>), grid, dim3(64), 0, stream, p); break;
+    case 16: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 16>), grid, dim3(64), 0, stream, p); break;
     default: set_error("MFMA decode: unsupported GQA group %d", p.G); return CF_ERR_UNSUPPORTED;
   }
   CF_HIP_CHECK(hipGetLastError());
@@ -867,8 +872,14 @@ void decode_mfma_bind_workspace(DecodeParams& p, void* workspace) {
 }
 
 bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
-  if (q_dt != kBF16) return false;
-  if (kv_dt != kBF16 && kv_dt != kE4M3) return false;
+  // bf16 queries over bf16 or e4m3 caches; fp16 queries over fp16 or e4m3
+  if (q_dt == kBF16) {
+    if (kv_dt != kBF16 && kv_dt != kE4M3) return false;
+  } else if (q_dt == kF16) {
+    if (kv_dt != kF16 && kv_dt != kE4M3) return false;
+  } else {
+    return false;
+  }
   if (p.bs != 16 || (p.D != 64 && p.D != 128)) return false;
   if (p.G != 1 && p.G != 2 && p.G != 4 && p.G != 8 && p.G != 16) return false;
   if (p.NB < 1) return false;  // invalid block ids are redirected to block 0 (then masked)
@@ -888,17 +899,17 @@ bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
   return true;
 }
 
-int32_t launch_decode_mfma(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream) {
-  (void)q_dt;
-  if (kv_dt == kE4M3) {
-    if (p.D == 128) return launch_t<kE4M3, 128>(p, stream);
-    if (p.D == 64) return launch_t<kE4M3, 64>(p, stream);
-  } else {
-    if (p.D == 128) return launch_t<kBF16, 128>(p, stream);
-    if (p.D == 64) return launch_t<kBF16, 64>(p, stream);
-  }
+template <int QT, int KT>
+int32_t launch_d(const DecodeParams& p, hipStream_t stream) {
+  if (p.D == 128) return launch_t<QT, KT, 128>(p, stream);
+  if (p.D == 64) return launch_t<QT, KT, 64>(p, stream);
   set_error("MFMA decode: unsupported head_dim %d", p.D);
   return CF_ERR_UNSUPPORTED;
+}
+
+int32_t launch_decode_mfma(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream) {
+  if (q_dt == kF16) return kv_dt == kE4M3 ? launch_d<kF16, kE4M3>(p, stream) : launch_d<kF16, kF16>(p, stream);
+  return kv_dt == kE4M3 ? launch_d<kBF16, kE4M3>(p, stream) : launch_d<kBF16, kBF16>(p, stream);
 }
 
 }  // namespace cf

@@ -20,6 +20,7 @@ namespace cf {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -58,6 +59,10 @@ struct KvTraits<kE4M3> {
 };
 template <>
 struct KvTraits<kBF16> {
+  static constexpr int kBytes = 2;
+};
+template <>
+struct KvTraits<kF16> {
   static constexpr int kBytes = 2;
 };
 
@@ -141,8 +146,6 @@ __device__ __forceinline__ bf16x8_t k_operand(const uint4* raw, int c) {
   }
 }
 
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-
 // 8 e4m3 codes -> 8 fp16 (exact: e4m3 values lie inside fp16's range and
 // precision).
 __device__ __forceinline__ f16x8_t e4m3x8_to_f16(uint32_t lo, uint32_t hi) {
@@ -155,6 +158,45 @@ __device__ __forceinline__ f16x8_t e4m3x8_to_f16(uint32_t lo, uint32_t hi) {
 }
 
 
+
+// Query-typed MFMA operands: bf16 queries multiply bf16 K (bf16 caches, or
+// e4m3 converted exactly); fp16 queries multiply fp16 K (fp16 caches, or
+// e4m3 converted exactly).
+template <int QT>
+using QOp = typename std::conditional<QT == kF16, f16x8_t, bf16x8_t>::type;
+
+template <int QT>
+__device__ __forceinline__ QOp<QT> as_qop(uint4 u) {
+  return __builtin_bit_cast(QOp<QT>, u);
+}
+
+template <int QT, int KT>
+__device__ __forceinline__ QOp<QT> k_operand_q(const uint4* raw, int c) {
+  if constexpr (QT == kF16) {
+    if constexpr (KT == kE4M3) {
+      const uint4 u = raw[c >> 1];
+      return (c & 1) ? e4m3x8_to_f16(u.z, u.w) : e4m3x8_to_f16(u.x, u.y);
+    } else {
+      return __builtin_bit_cast(f16x8_t, raw[c]);
+    }
+  } else {
+    return k_operand<KT>(raw, c);
+  }
+}
+
+__device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma16(f16x8_t a, f16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// fp32 -> the output's 16-bit code (round to nearest even).
+template <int QT>
+__device__ __forceinline__ uint16_t out_bits(float x) {
+  if constexpr (QT == kF16) return __builtin_bit_cast(uint16_t, (_Float16)x);
+  else return bf16_bits_from_f32(x);
+}
 
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll

@@ -56,7 +56,7 @@ def test_partition_sizes_agree(gpu, pt):
 
 @pytest.mark.parametrize("hq,hkv,d,bs", [(8, 8, 64, 16), (8, 2, 128, 16), (16, 1, 64, 16), (32, 2, 128, 16),
                                          (4, 4, 32, 8), (8, 2, 64, 32), (6, 3, 80, 16), (8, 4, 256, 16)])
-@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float8_e4m3fn])
 def test_shapes_and_dtypes(gpu, hq, hkv, d, bs, kv_dtype):
     print(f"[case] hq={hq} hkv={hkv} d={d} bs={bs} kv={kv_dtype}", flush=True)
     g = torch.Generator(device=gpu).manual_seed(hq * 1000 + d + bs)
@@ -68,15 +68,54 @@ def test_shapes_and_dtypes(gpu, hq, hkv, d, bs, kv_dtype):
         k = (n + bs - 1) // bs
         tables.append(perm[pos:pos + k])
         pos += k
-    q_dtype = torch.float32 if kv_dtype == torch.float32 else torch.bfloat16
+    q_dtype = kv_dtype if kv_dtype in (torch.float32, torch.float16) else torch.bfloat16
     q = torch.randn(b, hq, d, generator=g, device=gpu).to(q_dtype)
     ksrc = torch.randn(nb, bs, hkv, d, generator=g, device=gpu).to(q_dtype)
     vsrc = torch.randn(nb, bs, hkv, d, generator=g, device=gpu).to(q_dtype)
     case = workloads.DecodeCase("adhoc", q, ksrc, vsrc, tables, lens, bs, 1 / math.sqrt(d), kv_dtype)
     kc, vc, ks, vs = workloads.materialize(case, "native")
     out = _run(case, kc, vc, ks, vs, gpu, pt=4 * bs)
+    assert out.dtype == q_dtype
     ref = oracle_decode(case, kc, vc, ks, vs)
     assert_close(out.float().cpu().numpy(), ref, q_dtype, f"{hq}/{hkv}/{d}/{bs}/{kv_dtype}")
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 64)])
+def test_fp16_queries_take_the_mfma_path(gpu, hq, hkv, d, kv_dtype):
+    """fp16 queries over fp16 or e4m3 caches (block size 16, native layout)
+    run the MFMA kernel (fp16 operands) and match the float64 oracle; the
+    shared-prefix statement is exercised too."""
+    print(f"[case] fp16 q hq={hq} hkv={hkv} d={d} kv={kv_dtype}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(hq + d)
+    lens = [700, 1024, 1024 + 33, 40, 2000, 1]
+    nb = 600
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(9)).tolist()
+    shared = perm[:64]  # sequences 1 and 2 share a 1024-token prefix
+    tables, pos = [], 64
+    for i, n in enumerate(lens):
+        k = (n + 15) // 16
+        if i in (1, 2):
+            own = perm[pos:pos + k - 64]
+            pos += k - 64
+            tables.append(shared + own)
+        else:
+            tables.append(perm[pos:pos + k])
+            pos += k
+    q = torch.randn(len(lens), hq, d, generator=g, device=gpu).to(torch.float16)
+    ksrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.float16)
+    vsrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.float16)
+    case = workloads.DecodeCase("fp16", q, ksrc, vsrc, tables, lens, 16, 1 / math.sqrt(d), kv_dtype)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    sh = torch.tensor(ops.shared_prefix_lens(tables, lens, 16), dtype=torch.int32, device=gpu)
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    with ops.KernelTimer() as timer:
+        out = paged_attention_tensors(q, kc, vc, case.tables_tensor(gpu), case.seq_lens_tensor(gpu), 16, case.scale,
+                                      k_scale=ks, v_scale=vs, shared_prefix_lens=sh)
+        torch.cuda.synchronize()
+        assert timer.query("cf_decode_mfma")[1] == 1 and timer.query("cf_decode_generic")[1] == 0
+    assert out.dtype == torch.float16
+    assert_close(out.float().cpu().numpy(), ref, torch.float16, f"fp16 q / {kv_dtype}")
 
 
 def test_edge_lengths(gpu):
