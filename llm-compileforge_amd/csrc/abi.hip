@@ -171,14 +171,19 @@ static int64_t decode_max_parts(int64_t max_blocks, int32_t bs, int32_t pt) {
 // Partition length of the generic (VALU) path: the caller's, halved while the
 // launch would hold fewer than ~1k workgroups (small batches / few heads)
 // and a partition keeps at least max(block_size, 32) tokens, so short
-// batches still spread over the GPU.  A function of the call's sizes only:
-// the workspace query and the launch agree on it.
-static int32_t generic_partition(int64_t batch, int64_t num_kv_heads, int64_t max_blocks, int32_t bs, int32_t pt) {
+// batches still spread over the GPU; halved further (down to one block)
+// while a workgroup's scores would not fit its 64 KiB of LDS (many query
+// heads per KV head).  A function of the call's sizes only: the workspace
+// query and the launch agree on it.
+static int32_t generic_partition(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                 int64_t max_blocks, int32_t bs, int32_t pt) {
   const int64_t floor_tokens = std::max<int64_t>(bs, 32);
   int64_t t = pt;
   while (t / 2 >= floor_tokens && (t / 2) % bs == 0 &&
          batch * num_kv_heads * decode_max_parts(max_blocks, bs, (int32_t)t) < 1024)
     t /= 2;
+  const int64_t G = num_kv_heads > 0 ? num_q_heads / num_kv_heads : 1;
+  while (t / 2 >= bs && (t / 2) % bs == 0 && generic_lds_bytes(G, head_dim, t, bs) > 64 * 1024) t /= 2;
   return (int32_t)t;
 }
 
@@ -202,7 +207,8 @@ int32_t cf_paged_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int6
   CF_CHECK(block_size > 0 && partition_tokens > 0 && partition_tokens % block_size == 0,
            "partition_tokens (%d) must be a positive multiple of block_size (%d)", partition_tokens,
            block_size);
-  const int32_t gpt = generic_partition(batch, num_kv_heads, max_blocks_per_seq, block_size, partition_tokens);
+  const int32_t gpt = generic_partition(batch, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
+                                        partition_tokens);
   const int64_t parts = decode_max_parts(max_blocks_per_seq, block_size, gpt);
   const uint64_t generic = generic_workspace_bytes(batch, num_q_heads, head_dim, parts);
   const uint64_t mfma =
@@ -304,7 +310,7 @@ int32_t cf_paged_decode_shared(const CfTensor* q, const CfTensor* k_cache, const
   p.bs = block_size;
   p.Mb = (int)vt.size[1];
   p.NB = (int)NB;
-  p.PT = generic_partition(B, Hkv, vt.size[1], block_size, partition_tokens);
+  p.PT = generic_partition(B, Hq, Hkv, D, vt.size[1], block_size, partition_tokens);
   p.max_parts = (int)decode_max_parts(vt.size[1], block_size, p.PT);
 
   if (vk.dtype == CF_F8E4M3FN) {

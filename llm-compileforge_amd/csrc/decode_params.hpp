@@ -46,5 +46,7 @@ uint64_t decode_mfma_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t
 void decode_mfma_bind_workspace(DecodeParams& p, void* workspace);
 
 int32_t launch_decode_reduce(const DecodeParams& p, int q_dt, hipStream_t stream);
+// LDS bytes of one generic-kernel workgroup (G query heads, partition PT).
+size_t generic_lds_bytes(int64_t G, int64_t D, int64_t PT, int64_t bs);
 
 }  // namespace cf

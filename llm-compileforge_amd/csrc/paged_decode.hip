@@ -259,8 +259,7 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
 template <int QT, int KT>
 int32_t launch_generic_t(const DecodeParams& p, hipStream_t stream) {
   const dim3 grid(p.max_parts, p.Hkv, p.B);
-  const size_t sml_off = (size_t)p.G * p.D + (size_t)p.G * p.PT + (size_t)(((p.PT / p.bs + 1) & ~1));
-  const size_t lds = (sml_off + 2 * (size_t)p.G + kGenericThreads) * 4;
+  const size_t lds = generic_lds_bytes(p.G, p.D, p.PT, p.bs);
   if (lds > 64 * 1024) {
     set_error("generic decode needs %zu bytes of LDS (G=%d, D=%d, partition=%d); use a smaller partition",
               lds, p.G, p.D, p.PT);
@@ -299,6 +298,11 @@ int32_t launch_decode_generic(const DecodeParams& p, int q_dt, int kv_dt, hipStr
   }
   set_error("unsupported q dtype %d", q_dt);
   return CF_ERR_UNSUPPORTED;
+}
+
+size_t generic_lds_bytes(int64_t G, int64_t D, int64_t PT, int64_t bs) {
+  // q [G][D], scores [G][PT], block ids [PT / bs] (even), (m, l) [G][2], P.V sums [256]
+  return (size_t)(G * D + G * PT + ((PT / bs + 1) & ~1) + 2 * G + kGenericThreads) * 4;
 }
 
 int32_t launch_decode_reduce(const DecodeParams& p, int q_dt, hipStream_t stream) {

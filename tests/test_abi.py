@@ -206,6 +206,10 @@ def test_workspace_size_formula():
     assert n.value == generic_bytes(64, 32, 128, 2)
     assert lib.cf_paged_decode_workspace_bytes(1, 8, 8, 128, 2, 8, 512, ctypes.byref(n)) == 0
     assert n.value == 0  # 16 tokens: one partition at the 32-token floor, no workspace
+    # 64 query heads on one KV head: 512-token partitions would need 165 KB of LDS per
+    # workgroup, so the generic path halves them to 64 tokens (49 KB): 8192 / 64 partials
+    assert lib.cf_paged_decode_workspace_bytes(64, 64, 1, 128, 512, 16, 512, ctypes.byref(n)) == 0
+    assert n.value >= generic_bytes(64, 64, 128, 8192 // 64)
     # small batch (the opt-125m shape): 4 x 12 heads, 512 tokens -> partitions of 32 tokens
     assert lib.cf_paged_decode_workspace_bytes(4, 12, 12, 64, 32, 8, 512, ctypes.byref(n)) == 0
     assert n.value == generic_bytes(4, 12, 64, 256 // 32)

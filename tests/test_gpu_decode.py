@@ -260,6 +260,28 @@ def test_generic_path_many_partitions(gpu, kv_dtype, bs, d):
     assert_close(out.float().cpu().numpy(), ref, q_dtype, f"generic {kv_dtype}/{bs}/{d}")
 
 
+def test_generic_path_many_query_heads_per_kv_head(gpu):
+    """64 query heads over one fp32 KV head: the default 512-token partition
+    does not fit a workgroup's LDS, so the generic path shrinks it."""
+    print("[case] generic G=64", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(17)
+    lens, hq, hkv, d, bs = [3000, 77], 64, 1, 128, 16
+    nb = sum((n + bs - 1) // bs for n in lens) + 1
+    tables, pos = [], 0
+    for n in lens:
+        k = (n + bs - 1) // bs
+        tables.append(list(range(pos, pos + k)))
+        pos += k
+    q = torch.randn(len(lens), hq, d, generator=g, device=gpu)
+    ksrc = torch.randn(nb, bs, hkv, d, generator=g, device=gpu)
+    vsrc = torch.randn(nb, bs, hkv, d, generator=g, device=gpu)
+    case = workloads.DecodeCase("g64", q, ksrc, vsrc, tables, lens, bs, 1 / math.sqrt(d), torch.float32)
+    kc, vc, ks, vs = workloads.materialize(case, "native")
+    out = _run(case, kc, vc, ks, vs, gpu)
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    assert_close(out.float().cpu().numpy(), ref, torch.float32, "generic G=64")
+
+
 def test_repeated_calls_share_a_workspace(gpu):
     """Repeated calls on one workspace give bit-identical outputs, also after
     a call with another batch shape in between."""
