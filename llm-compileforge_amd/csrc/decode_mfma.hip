@@ -632,12 +632,15 @@ __device__ __forceinline__ int64_t part_row(int2 d, int k) {
 // run's, each a record or the wave slots of a split run.  One wave per
 // (h, b); partial rows hold the G heads of h in consecutive rows.
 template <int QT, int D, int G>
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
   constexpr int E = G * D / 64;  // output elements per lane
-  __shared__ float wgt[64][G];
-  __shared__ float inv_l[G];
+  constexpr int kWaves = 4;
+  __shared__ float wgt[kWaves][64][G];
+  __shared__ float part_acc[kWaves - 1][E][64];
+  __shared__ float part_ml[kWaves - 1][2][G];
   const int h = blockIdx.x, b = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform((int)threadIdx.x >> 6);
   const int2 dn = p.own_desc[(int64_t)b * p.Hkv + h];
   const int2 dp = p.pre_desc[(int64_t)b * p.Hkv + h];
   const int nown = dn.y < 0 ? 1 : dn.y;
@@ -646,6 +649,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
   if (nsrc == 0) return;  // written whole by the decode kernel (or empty)
   constexpr int KMAX = 64 / E;  // partials the register path holds
   if (nsrc <= KMAX) {
+    if (wave != 0) return;
     // Few partials (the usual case): every load is issued at once -- each
     // lane's slice of every partial row and every (m, l) -- so the merge
     // costs one round trip after the descriptors.
@@ -706,6 +710,9 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
     }
     return;
   }
+  // Many partials (a sequence split over hundreds of waves): wave w takes
+  // partials w, w + 4, w + 8, ... in groups of 64, keeping its own running
+  // (max, sum, output) per query head; then wave 0 combines the four.
   float acc[E];
 #pragma unroll
   for (int i = 0; i < E; ++i) acc[i] = 0.0f;
@@ -715,11 +722,10 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
     Mg[g] = -INFINITY;
     Lg[g] = 0.0f;
   }
-  // Partials are taken 64 at a time; the running max per head rescales what
-  // earlier rounds accumulated.
-  for (int k0 = 0; k0 < nsrc; k0 += 64) {
-    const int kn = min(64, nsrc - k0);
-    const int k = k0 + lane;
+  const int nloc = (nsrc - wave + kWaves - 1) / kWaves;  // this wave's partials
+  for (int j0 = 0; j0 < nloc; j0 += 64) {
+    const int kn = min(64, nloc - j0);
+    const int k = wave + kWaves * (j0 + lane);
     const int64_t row = k < nown ? part_row(dn, k) : part_row(dp, k - nown);
     float m[G], l[G];
 #pragma unroll
@@ -741,37 +747,87 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
       const float wk = (m[g] == -INFINITY) ? 0.0f : __expf(m[g] - mnew);
       Lg[g] = Lg[g] * scale_old[g] + wave_sum(l[g] * wk);
       Mg[g] = mnew;
-      if (lane < kn) wgt[lane][g] = wk;
+      if (lane < kn) wgt[wave][lane][g] = wk;
     }
-    __syncthreads();
+    // the weights pass between lanes of this wave only
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int i = 0; i < E; ++i) acc[i] *= scale_old[(lane + 64 * i) / D];
-    for (int kk = 0; kk < kn; ++kk) {
-      const int ks = k0 + kk;
-      const int64_t rk = ks < nown ? part_row(dn, ks) : part_row(dp, ks - nown);
-      const float* o = p.ws_o + rk * D;
+    // U partial rows per step, all their loads issued before the sums
+    constexpr int U = E <= 8 ? 8 : (E <= 16 ? 4 : 2);
+    for (int kk = 0; kk < kn; kk += U) {
+      float ov[U][E];
 #pragma unroll
-      for (int i = 0; i < E; ++i) {
-        const int idx = lane + 64 * i;
-        acc[i] += wgt[kk][idx / D] * o[idx];
+      for (int u = 0; u < U; ++u) {
+        const int ks = wave + kWaves * (j0 + kk + u);
+        if (kk + u < kn) {
+          const int64_t rk = ks < nown ? part_row(dn, ks) : part_row(dp, ks - nown);
+          const float* o = p.ws_o + rk * D;
+#pragma unroll
+          for (int i = 0; i < E; ++i) ov[u][i] = o[lane + 64 * i];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kk + u < kn) {
+#pragma unroll
+          for (int i = 0; i < E; ++i) acc[i] += wgt[wave][kk + u][(lane + 64 * i) / D] * ov[u][i];
+        }
       }
     }
-    __syncthreads();
+    // the next group overwrites this wave's weights
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  if (lane < G) {
-    float lg = 0.0f;
+  if (wave > 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-      if (g == lane) lg = Lg[g];
-    inv_l[lane] = lg > 0.0f ? 1.0f / lg : 0.0f;
+    for (int i = 0; i < E; ++i) part_acc[wave - 1][i][lane] = acc[i];
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        part_ml[wave - 1][0][g] = Mg[g];
+        part_ml[wave - 1][1][g] = Lg[g];
+      }
+    }
   }
   __syncthreads();
+  if (wave != 0) return;
+  // combine: M = max of the waves' maxima, each wave's (L, acc) scaled to it
+  float sw[kWaves][G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float M = Mg[g];
+#pragma unroll
+    for (int w2 = 0; w2 < kWaves - 1; ++w2) M = fmaxf(M, part_ml[w2][0][g]);
+    sw[0][g] = Mg[g] == -INFINITY ? 0.0f : __expf(Mg[g] - M);
+    float L = Lg[g] * sw[0][g];
+#pragma unroll
+    for (int w2 = 0; w2 < kWaves - 1; ++w2) {
+      const float mw = part_ml[w2][0][g];
+      sw[w2 + 1][g] = mw == -INFINITY ? 0.0f : __expf(mw - M);
+      L += part_ml[w2][1][g] * sw[w2 + 1][g];
+    }
+    Lg[g] = L;
+  }
   uint16_t* out = (uint16_t*)p.out + (int64_t)b * p.o_sb;
 #pragma unroll
   for (int i = 0; i < E; ++i) {
     const int idx = lane + 64 * i;
     const int g = idx / D, d = idx % D;
-    out[(int64_t)(h * G + g) * p.o_sh + d] = out_bits<QT>(acc[i] * inv_l[g]);
+    float a = 0.0f, lg = 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) {
+      if (gg == g) {
+        a = acc[i] * sw[0][gg];
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves - 1; ++w2) a += part_acc[w2][i][lane] * sw[w2 + 1][gg];
+        lg = Lg[gg];
+      }
+    }
+    out[(int64_t)(h * G + g) * p.o_sh + d] = out_bits<QT>(lg > 0.0f ? a / lg : 0.0f);
   }
 }
 
@@ -826,11 +882,11 @@ int32_t launch_t(const DecodeParams& p, hipStream_t stream) {
   const dim3 grid(p.Hkv, p.B);
   ProfileScope prof("cf_decode_merge", stream);
   switch (p.G) {
-    case 1: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 1>), grid, dim3(64), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 2>), grid, dim3(64), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 4>), grid, dim3(64), 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 8>), grid, dim3(64), 0, stream, p); break;
-    case 16: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 16>), grid, dim3(64), 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 1>), grid, dim3(256), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 2>), grid, dim3(256), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 4>), grid, dim3(256), 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 8>), grid, dim3(256), 0, stream, p); break;
+    case 16: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 16>), grid, dim3(256), 0, stream, p); break;
     default: set_error("MFMA decode: unsupported GQA group %d", p.G); return CF_ERR_UNSUPPORTED;
   }
   CF_HIP_CHECK(hipGetLastError());
