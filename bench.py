@@ -342,7 +342,7 @@ def main() -> None:
     ap.add_argument("--config", default="c3_llama3_8b")
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--partition", type=int, default=512)
-    ap.add_argument("--layout", default="native")
+    ap.add_argument("--layout", default="paired")
     ap.add_argument("--pools", type=int, default=2, help="cache copies rotated between steps")
     ap.add_argument("--cpu-sample", type=int, default=8)
     ap.add_argument("--cpu-budget", type=float, default=10.0)

@@ -170,7 +170,7 @@ def make_case(config: str, device: torch.device | str = "cpu", seed: int = 0, ba
     return DecodeCase(config, q, k, v, tables, lens, bs, 1.0 / math.sqrt(d), kv_dtype, meta)
 
 
-def materialize(case: DecodeCase, layout: str = "native"):
+def materialize(case: DecodeCase, layout: str = "paired"):
     """Device caches for `case`: (k_cache, v_cache, k_scale, v_scale).
 
     e4m3 configs quantize the sources with per-KV-head scales (amax over the
@@ -321,7 +321,7 @@ def _int_tensor(rows: list[list[int]], device) -> torch.Tensor:
     return out.to(device)
 
 
-def materialize_mixed(case: MixedCase, layout: str = "native") -> dict[str, torch.Tensor | None]:
+def materialize_mixed(case: MixedCase, layout: str = "paired") -> dict[str, torch.Tensor | None]:
     """Device tensors of the step: the cache before the step (e4m3 with
     scales calibrated over pool and new rows, or bf16) and every input of
     the write, decode and prefill calls."""

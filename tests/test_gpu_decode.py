@@ -32,7 +32,7 @@ def _run(case, kc, vc, ks, vs, dev, pt=512, tables=None, lens=None):
     return out
 
 
-@pytest.mark.parametrize("layout", ["native", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "native", "token_major"])
 @pytest.mark.parametrize("config,batch", [("c1_opt125m", None), ("c2_tinyllama", None), ("c3_llama3_8b", 6),
                                           ("c4_llama3_70b", 3)])
 def test_configs_match_oracle(gpu, config, batch, layout):

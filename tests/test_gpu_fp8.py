@@ -88,7 +88,7 @@ def test_reference_fp8_cases_on_device(gpu):
     assert not quant.check_hardware_support("NVIDIA A100") and not quant.check_hardware_support("CPU")
 
 
-@pytest.mark.parametrize("layout", ["native", "token_major"])
+@pytest.mark.parametrize("layout", ["paired", "native", "token_major"])
 @pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
 def test_kv_write_bit_exact(gpu, layout, slot_dtype):
     nb, bs, h, d, t = 40, 16, 8, 128, 300

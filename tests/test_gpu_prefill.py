@@ -77,12 +77,13 @@ def _prefill(case, t, **kw):
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 1, 128), (32, 2, 64), (4, 2, 128),
                                       (16, 8, 64)])
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
-def test_shapes_match_oracle(gpu, hq, hkv, d, kv_dtype):
-    print(f"[case] prefill hq={hq} hkv={hkv} d={d} kv={kv_dtype}", flush=True)
+@pytest.mark.parametrize("layout", ["paired", "native"])
+def test_shapes_match_oracle(gpu, hq, hkv, d, kv_dtype, layout):
+    print(f"[case] prefill hq={hq} hkv={hkv} d={d} kv={kv_dtype} layout={layout}", flush=True)
     case = workloads.make_mixed_case(device=gpu, seed=hq + d, chunks=[1, 17, 64, 100, 33],
                                      cached=[0, 5, 300, 33, 1000], decode_lens=[], num_q_heads=hq,
                                      num_kv_heads=hkv, head_dim=d, kv_dtype=kv_dtype)
-    t = workloads.materialize_mixed(case)
+    t = workloads.materialize_mixed(case, layout)
     _write_new_rows(case, t)
     out = _prefill(case, t)
     ref, covered = oracle_prefill(case, t)

@@ -103,10 +103,25 @@ def test_layouts(dtype):
     assert v.stride() == (4 * 32 * 16, 1, 32 * 16, 16)
     assert L.layout_of(k, False) == "native" and L.layout_of(v, True) == "native"
     src = torch.randn(5, 16, 4, 32)
-    for lay in L.LAYOUTS:
+    for lay in ("native", "token_major"):
         for is_v in (False, True):
             t = L.to_layout(src, lay, is_v)
             assert torch.equal(t, src) and L.layout_of(t, is_v) == lay
+    # paired: one allocation, (block, head) = K tile [bs][D] then V tile [D][bs]
+    kp, vp = L.alloc_kv_cache(5, 16, 4, 32, dtype, "cpu", "paired")
+    assert kp.stride() == (4 * 2 * 16 * 32, 32, 2 * 16 * 32, 1)
+    assert vp.stride() == (4 * 2 * 16 * 32, 1, 2 * 16 * 32, 16)
+    assert vp.data_ptr() - kp.data_ptr() == 16 * 32 * kp.element_size()
+    assert L.layout_of(kp, False) == "paired" and L.layout_of(vp, True) == "paired"
+    vsrc = torch.randn(5, 16, 4, 32)
+    kp, vp = L.to_paired(src.to(dtype), vsrc.to(dtype))
+    assert torch.equal(kp.float(), src.to(dtype).float()) and torch.equal(vp.float(), vsrc.to(dtype).float())
+    # block 2, head 3, token 5, channel 7 of K and of V, read from the raw storage
+    raw = kp.as_strided((5 * 4 * 2 * 16 * 32,), (1,), kp.storage_offset()).view(5, 4, 2, 16 * 32)
+    assert torch.equal(raw[2, 3, 0, 5 * 32 + 7].float(), kp[2, 5, 3, 7].float())
+    assert torch.equal(raw[2, 3, 1, 7 * 16 + 5].float(), vp[2, 5, 3, 7].float())
+    with pytest.raises(ValueError):
+        L.to_layout(src, "paired", False)
     with pytest.raises(ValueError):
         L.alloc_kv_cache(1, 16, 1, 8, torch.float32, "cpu", "bogus")
 
