@@ -495,7 +495,13 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   int run_j0 = c0.j;
   bool first_run = true;
 
+  QOp<QT> qnext[NC];  // the next run's q columns, loaded a tile ahead
   for (;;) {
+    // A run ends with this tile: the next run's q loads go out now, ahead
+    // of the next tile's K/V, so they have landed when that tile computes
+    // (a load issued after the flush would stall it a full round trip).
+    const bool run_ends = !has1 || c1.b != c0.b || c1.h != c0.h || c1.kind != c0.kind;
+    if (has1 && run_ends) load_q<QT, D>(qnext, p, c1, li, lq);
     // Always issue the next tile's loads (the last iteration reloads its
     // own tile) so every path has the same number of loads in flight and
     // the compiler's vmcnt waits stay exact.
@@ -594,7 +600,6 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     }
 
     // ---- end of a run -----------------------------------------------------
-    const bool run_ends = !has1 || c1.b != c0.b || c1.h != c0.h || c1.kind != c0.kind;
     if (run_ends) {
       flush_run<QT, PL, D>(p, ix, pl, c0, o, m, l, run_j0, first_run, tau, chunk, w, lane);
       first_run = false;
@@ -607,7 +612,8 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     r0 = r1;
     ++tau;
     if (run_ends) {
-      load_q<QT, D>(qop, p, c0, li, lq);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) qop[cc] = qnext[cc];
       m = -INFINITY;
       l = 0.0f;
 #pragma unroll
