@@ -47,11 +47,12 @@ namespace {
 // Within a KV head, runs are laid out sequence by sequence: a group
 // leader's prefix run (its group's shared tiles), then each sequence's own
 // run (its tiles after the shared prefix, all of them outside a group).
-// The stream is (KV head, run, tile); with Tb tiles per head and
-// T = Hkv * Tb in all, wave w of the Wtot launched waves takes the
-// contiguous range [w * chunk, min((w + 1) * chunk, T)), chunk = ceil(T /
-// Wtot): every wave gets the same number of tiles whatever the length mix,
-// and no workgroup is launched for nothing.  Inside its range a wave keeps
+// The stream is (KV head, run, tile), each run preceded by kRunPad empty
+// slots (planned launches); with Tb slots per head and T = Hkv * Tb in all,
+// wave w of the Wtot launched waves takes the slots [w * chunk,
+// min((w + 1) * chunk, T)), chunk = ceil(T / Wtot): every wave gets the
+// same amount of work (tiles plus run changes) whatever the length mix, and
+// no workgroup is launched for nothing.  Inside its range a wave keeps
 // one online-softmax state per run.  A run the wave holds whole is written
 // out: normalized to the output (a sequence outside any group), or as an
 // (m, l, o) record (a group member's own run, a prefix run).  A run split
@@ -69,6 +70,14 @@ namespace {
 // ---------------------------------------------------------------------------
 
 constexpr int kPlanMaxB = 2048;    // batches up to this size keep a per-sequence plan in LDS
+// Stream slots a run's start costs in planned launches.  Ending one run and
+// starting the next (flush, new table rows, new q columns) takes about as
+// long as one to two tiles (per-wave timings on the Llama-3-8B shape: 1.2 us
+// a tile, 1.6 us a run), so each run is preceded by kRunPad empty slots and
+// waves split the padded stream evenly: a wave whose range crosses several
+// run boundaries gets correspondingly fewer tiles.  2 measured faster than
+// 1 or 3.
+constexpr int kRunPad = 2;
 constexpr int kMinShareTiles = 2;  // shortest shared prefix (32-token tiles) given a group run
 constexpr int kSlotCols = 16;      // columns of one partial slot (the MFMA width)
 constexpr int kOwn = 0, kPrefix = 1;
@@ -154,7 +163,8 @@ __device__ void plan_pass2(const DecodeParams& p, Plan* pl, int lane) {
 }
 
 // Pass 3: j0 <- the group's shared tiles; psum <- exclusive scan of the
-// tiles of each sequence's runs (prefix run for leaders + own run).
+// stream slots of each sequence's runs (prefix run for leaders + own run),
+// kRunPad + tiles per run.
 __device__ void plan_pass3(const DecodeParams& p, Plan* pl, int lane) {
   int carry = 0;
   for (int base = 0; base < p.B; base += 64) {
@@ -163,7 +173,8 @@ __device__ void plan_pass3(const DecodeParams& p, Plan* pl, int lane) {
     if (b < p.B) {
       const int lead = pl->psum[b];
       j0 = pl->pre[lead] & 0xFFFFFF;
-      rt = (lead == b ? j0 : 0) + ((pl->len[b] + 31) >> 5) - j0;
+      const int own = ((pl->len[b] + 31) >> 5) - j0;
+      rt = (lead == b && j0 > 0 ? kRunPad + j0 : 0) + (own > 0 ? kRunPad + own : 0);
     }
     const int incl = wave_incl_scan(rt, lane) + carry;
     if (b < p.B) {
@@ -175,7 +186,8 @@ __device__ void plan_pass3(const DecodeParams& p, Plan* pl, int lane) {
   if (lane == 0) pl->psum[p.B] = carry;
 }
 
-// Largest b with psum[b] <= r (64-ary search; psum[0] = 0 <= r).
+// Largest b with psum[b] <= r (64-ary search; psum[0] = 0 <= r): the
+// sequence whose runs hold stream slot r.
 __device__ int plan_find(const Plan* pl, int B, int r, int lane) {
   int lo = 0, n = B;
   while (n > 1) {
@@ -243,7 +255,8 @@ struct Seqs {
     if constexpr (PL) return uniform(pl->pre[b]);
     else return 0;
   }
-  __device__ __forceinline__ int run_tiles(int b) const {
+  // stream slots of sequence b's runs (0: it has none)
+  __device__ __forceinline__ int run_slots(int b) const {
     if constexpr (PL) return uniform(pl->psum[b + 1] - pl->psum[b]);
     else return (len(b) + 31) >> 5;
   }
@@ -256,6 +269,7 @@ struct Coord {
   int len;          // effective length of sequence b
   int ncols;        // MFMA columns in use: G, or members * G for a prefix run
   int blkA, blkB;   // physical blocks of the tile (-1: none / invalid)
+  int64_t v;        // the tile's stream slot
 };
 
 __device__ __forceinline__ int checked_block(const DecodeParams& p, const Index& ix, int b, int jb) {
@@ -294,9 +308,18 @@ __device__ __forceinline__ void enter_seq(const Seqs<PL>& s, Coord& c, int b, in
   }
 }
 
+// Stream slot of the tile after c (the next run's first tile when c ends
+// its run).
+template <bool PL>
+__device__ __forceinline__ int64_t next_slot(const Coord& c) {
+  constexpr int pad = PL ? kRunPad : 0;
+  return c.v + 1 + (c.j + 1 < c.last ? 0 : pad);
+}
+
 // Next tile in stream order (the caller knows one exists).
 template <bool PL>
 __device__ __forceinline__ Coord advance(const DecodeParams& p, const Index& ix, const Seqs<PL>& s, Coord c) {
+  c.v = next_slot<PL>(c);
   if (c.j + 1 < c.last) {
     c.j += 1;
   } else if (c.kind == kPrefix && c.last < ((c.len + 31) >> 5)) {
@@ -309,7 +332,7 @@ __device__ __forceinline__ Coord advance(const DecodeParams& p, const Index& ix,
         b = 0;
         c.h += 1;
       }
-    } while (s.run_tiles(b) == 0);
+    } while (s.run_slots(b) == 0);
     enter_seq(s, c, b, p.G);
   }
   fetch_ids(p, ix, c);
@@ -339,7 +362,8 @@ __device__ __forceinline__ void load_q(QOp<QT>* qop, const DecodeParams& p, cons
 template <int QT, bool PL, int D>
 __device__ __forceinline__ void flush_run(const DecodeParams& p, const Index& ix, const Plan* pl, const Coord& c,
                                           const f32x4_t* o, float m, float l, int run_j0, bool first_run,
-                                          int64_t tau, int64_t chunk, int w, int lane) {
+                                          int64_t chunk, int w, int lane) {
+  constexpr int pad = PL ? kRunPad : 0;
   constexpr int NV = D / 16;
   const int li = lane & 15, lq = lane >> 4;
   const int G = p.G;
@@ -353,12 +377,13 @@ __device__ __forceinline__ void flush_run(const DecodeParams& p, const Index& ix
   if (holds_first) {
     int2 d = make_int2(0, 0);
     if (!complete) {
-      // the run's stream tiles [s_tile, s_tile + len) span waves w1..w2; w1
-      // holds it in slot 1 unless the run starts its range
-      const int64_t s_tile = tau - (c.j - c.first);
+      // the run's tiles, stream slots [s_tile, s_tile + len), span waves
+      // w1..w2; w1 holds it in slot 1 when its range also holds the
+      // previous run's last tile (slot s_tile - pad - 1), else in slot 0
+      const int64_t s_tile = c.v - (c.j - c.first);
       const int64_t w1 = s_tile / chunk;
       const int64_t w2 = (s_tile + (c.last - c.first) - 1) / chunk;
-      d = make_int2((int)((w1 * 2 + (w1 * chunk < s_tile ? 1 : 0)) * kSlotCols), (int)(w2 - w1 + 1));
+      d = make_int2((int)((w1 * 2 + (s_tile - pad - 1 >= w1 * chunk ? 1 : 0)) * kSlotCols), (int)(w2 - w1 + 1));
     }
     if (c.kind == kOwn) {
       if (lane == 0) {
@@ -452,34 +477,39 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   const int64_t T = (int64_t)p.Hkv * Tb;
   if (T == 0) return;
   const int64_t chunk = (T + Wtot - 1) / Wtot;
-  int64_t tau = (int64_t)w * chunk;
-  if (tau >= T) return;
-  const int64_t tau_end = tau + chunk < T ? tau + chunk : T;
+  const int64_t v0 = (int64_t)w * chunk;  // this wave's stream slots [v0, v_end)
+  if (v0 >= T) return;
+  const int64_t v_end = v0 + chunk < T ? v0 + chunk : T;
 
   Coord c0;
-  c0.h = uniform((int)(tau / Tb));
+  c0.h = uniform((int)(v0 / Tb));
   {
-    const int r = uniform((int)(tau % Tb));
+    const int r = uniform((int)(v0 % Tb));
     if constexpr (PL) {
+      // slot r: a run's padding (start at that run's first tile) or a tile
       const int b = plan_find(pl, p.B, r, lane);
-      const int o = r - uniform(pl->psum[b]);
+      int o = r - uniform(pl->psum[b]);
+      int vrun = uniform(pl->psum[b]);
       enter_seq(seqs, c0, b, p.G);
-      if (c0.kind == kPrefix && o >= c0.last) {
+      if (c0.kind == kPrefix && o >= kRunPad + c0.last) {
+        o -= kRunPad + c0.last;
+        vrun += kRunPad + c0.last;
         own_run(c0, c0.last, p.G);
-        c0.j = c0.first + (o - (int)(seqs.pre(b) & 0xFFFFFF));
-      } else {
-        c0.j = c0.first + o;
       }
+      c0.j = c0.first + (o > kRunPad ? o - kRunPad : 0);
+      c0.v = (int64_t)c0.h * Tb + vrun + kRunPad + (c0.j - c0.first);
     } else {
       int b, before;
       locate(p, ix, r, lane, &b, &before);
       enter_seq(seqs, c0, b, p.G);
       c0.j = r - before;
+      c0.v = v0;
     }
   }
+  if (c0.v >= v_end) return;  // the range holds padding only
   fetch_ids(p, ix, c0);
   Coord c1 = c0;
-  bool has1 = tau + 1 < tau_end;
+  bool has1 = next_slot<PL>(c0) < v_end;
   if (has1) c1 = advance(p, ix, seqs, c0);
 
   const KvCacheView kv{(const uint8_t*)p.k, (const uint8_t*)p.v, p.k_s[0], p.k_s[2], p.v_s[0], p.v_s[2]};
@@ -506,7 +536,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     // own tile) so every path has the same number of loads in flight and
     // the compiler's vmcnt waits stay exact.
     load_tile<KT, D>(r1, kv, c1.blkA, c1.blkB, li, lq, c1.h);
-    const bool has2 = has1 && tau + 2 < tau_end;
+    const bool has2 = has1 && next_slot<PL>(c1) < v_end;
     Coord c2 = c1;
     if (has2) c2 = advance(p, ix, seqs, c1);
 
@@ -601,7 +631,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
 
     // ---- end of a run -----------------------------------------------------
     if (run_ends) {
-      flush_run<QT, PL, D>(p, ix, pl, c0, o, m, l, run_j0, first_run, tau, chunk, w, lane);
+      flush_run<QT, PL, D>(p, ix, pl, c0, o, m, l, run_j0, first_run, chunk, w, lane);
       first_run = false;
     }
     if (!has1) break;
@@ -610,7 +640,6 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     c1 = c2;
     has1 = has2;
     r0 = r1;
-    ++tau;
     if (run_ends) {
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) qop[cc] = qnext[cc];
