@@ -200,6 +200,13 @@ int32_t cf_prefill_chunk_fp8(const CfTensor* q, const CfTensor* k_cache,
  *   scales  [H]         f32 (output, contiguous) */
 int32_t cf_fp8_amax_scale(const CfTensor* x, CfTensor* scales, void* stream);
 
+/* The same per-KV-head scale computation under the name the K/V-cache
+ * callers use (quantize_block's scale rule, reference
+ * compiler/quantize/fp8_kv_cache.py:81-86, per KV head):
+ * scales_out[h] = amax(|x[..., h, :]|) / 448, >= 1e-12, 1.0 for an
+ * all-zero head.  Arguments as cf_fp8_amax_scale. */
+int32_t cf_kv_amax_scale(const CfTensor* x, CfTensor* scales_out, void* stream);
+
 /* out[t,h,d] = e4m3fn(f32(x[t,h,d]) / scales[h]) with IEEE division and
  * round-to-nearest-even, |v| >= 480 -> NaN code (torch's float8_e4m3fn
  * conversion).  Reference compiler/quantize/fp8_kv_cache.py:89.
@@ -333,21 +340,13 @@ int32_t cf_block_tables_apply(CfTensor* table, CfTensor* lens, const CfTensor* d
  * copy-on-write.  A destination must not be another pair's source. */
 int32_t cf_copy_blocks(CfTensor* cache, const CfTensor* pairs, void* stream);
 
-/* HBM read probe for measurement (no reference counterpart): `waves`
- * independent waves (a multiple of 4) each read chunks_per_wave whole
- * chunks of chunk_bytes at chunk_ids[w * chunks_per_wave + i] of buf (ids
- * in [0, buf_bytes / chunk_bytes), trusted); `sink` (waves * 64 u32) is
- * practically never written.  Gives the practical read rate for the decode
- * kernel's access shape. */
-int32_t cf_hbm_read_probe(const void* buf, int64_t buf_bytes, const int32_t* chunk_ids,
-                          int64_t waves, int64_t chunks_per_wave, int64_t chunk_bytes,
-                          uint32_t* sink, void* stream);
-
 /* Kernel timing hook for benchmarks (no reference counterpart).  While
- * enabled, every kernel this library launches is bracketed by a pair of
- * HIP events recorded on the launch stream.  cf_profile_query synchronizes
- * on the recorded events and returns the summed duration (ms) and launch
- * count of kernels whose name starts with `prefix`. */
+ * enabled, every kernel this library launches carries a pair of HIP events
+ * that the launch itself stamps with the kernel's start and end
+ * (hipExtLaunchKernel: no marker packets are added to the stream, so the
+ * kernels run back to back as they do without the hook).  cf_profile_query
+ * synchronizes on the recorded events and returns the summed duration (ms)
+ * and launch count of kernels whose name starts with `prefix`. */
 int32_t cf_profile_enable(int32_t on);
 int32_t cf_profile_reset(void);
 int32_t cf_profile_query(const char* prefix, double* total_ms,

@@ -158,6 +158,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          ctypes.c_void_p],
     ),
     "cf_fp8_amax_scale": (ctypes.c_int32, [_P, _P, ctypes.c_void_p]),
+    "cf_kv_amax_scale": (ctypes.c_int32, [_P, _P, ctypes.c_void_p]),
     "cf_fp8_quantize": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
     "cf_fp8_dequantize": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
     "cf_kv_write_fp8": (ctypes.c_int32, [_P, _P, _P, _P, _P, _P, _P, ctypes.c_void_p]),
@@ -190,8 +191,6 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "cf_bp_shared_prefix_lens": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
     "cf_block_tables_apply": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
     "cf_copy_blocks": (ctypes.c_int32, [_P, _P, ctypes.c_void_p]),
-    "cf_hbm_read_probe": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
-                                           ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]),
     "cf_profile_enable": (ctypes.c_int32, [ctypes.c_int32]),
     "cf_profile_reset": (ctypes.c_int32, []),
     "cf_profile_query": (

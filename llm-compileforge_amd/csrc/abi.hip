@@ -89,20 +89,55 @@ hipEvent_t take_event() {
 
 bool profiling_enabled() { return g_prof_on; }
 
-int profile_begin(const char* name, hipStream_t stream) {
-  if (!g_prof_on) return -1;
+namespace {
+// Events armed by a ProfileScope for this thread's next launch.
+struct Pending {
+  std::string name;
+  hipEvent_t begin = nullptr, end = nullptr;
+};
+thread_local Pending g_pending;
+
+void release_pending() {
+  if (g_pending.begin) g_prof_pool.push_back(g_pending.begin);
+  if (g_pending.end) g_prof_pool.push_back(g_pending.end);
+  g_pending = Pending{};
+}
+}  // namespace
+
+void profile_arm(const char* name) {
+  if (!g_prof_on) return;
   std::lock_guard<std::mutex> lock(g_prof_mu);
-  ProfRecord rec{name, take_event(), take_event()};
-  if (!rec.begin || !rec.end) return -1;
-  if (hipEventRecord(rec.begin, stream) != hipSuccess) return -1;
-  g_prof_records.push_back(rec);
-  return (int)g_prof_records.size() - 1;
+  release_pending();
+  hipEvent_t b = take_event(), e = take_event();
+  if (!b || !e) {
+    if (b) g_prof_pool.push_back(b);
+    if (e) g_prof_pool.push_back(e);
+    return;
+  }
+  g_pending.name = name;
+  g_pending.begin = b;
+  g_pending.end = e;
 }
 
-void profile_end(int slot, hipStream_t stream) {
-  if (slot < 0) return;
+void profile_disarm() {
+  if (!g_pending.begin && !g_pending.end) return;
   std::lock_guard<std::mutex> lock(g_prof_mu);
-  if (slot < (int)g_prof_records.size()) (void)hipEventRecord(g_prof_records[slot].end, stream);
+  release_pending();
+}
+
+hipEvent_t profile_take_begin() {
+  if (!g_pending.begin) return nullptr;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  g_prof_records.push_back(ProfRecord{g_pending.name, g_pending.begin, g_pending.end});
+  hipEvent_t b = g_pending.begin;
+  g_pending.begin = nullptr;
+  return b;
+}
+
+hipEvent_t profile_take_end() {
+  hipEvent_t e = g_pending.end;
+  g_pending = Pending{};
+  return e;
 }
 
 namespace {
@@ -484,6 +519,10 @@ int32_t cf_fp8_amax_scale(const CfTensor* x, CfTensor* scales, void* stream) {
            "x too large");
   if (x4.size[2] == 0) return CF_OK;
   return launch_amax_scale(x4, vx.dtype, (float*)vsc.base, 1, as_stream(stream));
+}
+
+int32_t cf_kv_amax_scale(const CfTensor* x, CfTensor* scales_out, void* stream) {
+  return cf_fp8_amax_scale(x, scales_out, stream);
 }
 
 int32_t cf_fp8_quantize(const CfTensor* x, const CfTensor* scales, CfTensor* out, void* stream) {

@@ -543,7 +543,7 @@ int32_t cf_block_tables_apply(CfTensor* table, CfTensor* lens, const CfTensor* d
   const int64_t n = vd.size[0];
   if (n == 0) return CF_OK;
   ProfileScope prof("cf_block_tables_apply", (hipStream_t)stream);
-  hipLaunchKernelGGL(table_apply_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+  CF_LAUNCH(table_apply_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                      (int32_t*)vt.base, vt.stride[0], vt.stride[1], (int32_t*)vl.base, vl.stride[0],
                      (const int32_t*)vd.base, vd.stride[0], vd.stride[1], n, vt.size[0], vt.size[1]);
   CF_HIP_CHECK(hipGetLastError());
@@ -567,7 +567,7 @@ int32_t cf_copy_blocks(CfTensor* cache, const CfTensor* pairs, void* stream) {
   const int64_t per = vec ? bytes / 16 : bytes;
   const unsigned gx = (unsigned)std::min<int64_t>(std::max<int64_t>((per + 255) / 256, 1), 64);
   ProfileScope prof("cf_copy_blocks", (hipStream_t)stream);
-  hipLaunchKernelGGL(copy_blocks_kernel, dim3(gx, (unsigned)n), dim3(256), 0, (hipStream_t)stream, vc.base, stride,
+  CF_LAUNCH(copy_blocks_kernel, dim3(gx, (unsigned)n), dim3(256), 0, (hipStream_t)stream, vc.base, stride,
                      bytes, (const int32_t*)vp.base, vp.stride[0], vp.stride[1], vc.size[0], vec);
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;

@@ -2,6 +2,7 @@
 // kernel-launch profiling.  Internal to libcf_hip.so.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -81,18 +82,32 @@ inline const char* dtype_name(int dt) {
 int32_t view_of(const CfTensor* t, const char* name, int rank, View* v);
 
 // ---- launch profiling ---------------------------------------------------
+// While the timing hook (cf_profile_enable) is on, a ProfileScope arms a
+// pair of HIP events for the next CF_LAUNCH on this thread.  The launch
+// hands them to hipExtLaunchKernel, which stamps them with the kernel's own
+// start and end (no marker packets are added to the stream), so the
+// measured duration is the kernel's execution time.
 bool profiling_enabled();
-// Records the "begin" event for a launch of kernel `name` on `stream` and
-// returns a slot id (or -1 when disabled); profile_end records the "end".
-int profile_begin(const char* name, hipStream_t stream);
-void profile_end(int slot, hipStream_t stream);
+// Arms events for kernel `name` (no-op when profiling is off).
+void profile_arm(const char* name);
+// Disarms events the launch did not consume (error paths).
+void profile_disarm();
+// The armed events (nullptr when none); registers the launch's record.
+hipEvent_t profile_take_begin();
+hipEvent_t profile_take_end();
 
 struct ProfileScope {
-  int slot;
-  hipStream_t stream;
-  ProfileScope(const char* name, hipStream_t s) : slot(profile_begin(name, s)), stream(s) {}
-  ~ProfileScope() { profile_end(slot, stream); }
+  ProfileScope(const char* name, hipStream_t) { profile_arm(name); }
+  ~ProfileScope() { profile_disarm(); }
 };
+
+// Kernel launch on `stream`, carrying the armed timing events if any.
+#define CF_LAUNCH(kernel, grid, block, lds, stream, ...)                                                \
+  do {                                                                                                 \
+    hipEvent_t cf_b_ = ::cf::profile_take_begin();                                                     \
+    hipEvent_t cf_e_ = ::cf::profile_take_end();                                                       \
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, cf_b_, cf_e_, 0, __VA_ARGS__);              \
+  } while (0)
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -903,7 +903,7 @@ template <int QT, int KT, int D, bool PL>
 int32_t launch_stream_t(const DecodeParams& p, hipStream_t stream) {
   const int blocks = cu_count() * blocks_per_cu<QT, KT, D, PL>();
   ProfileScope prof("cf_decode_mfma", stream);
-  hipLaunchKernelGGL((decode_stream_kernel<QT, KT, D, PL>), dim3(blocks), dim3(256), PL ? sizeof(Plan) : 0, stream, p,
+  CF_LAUNCH((decode_stream_kernel<QT, KT, D, PL>), dim3(blocks), dim3(256), PL ? sizeof(Plan) : 0, stream, p,
                      p.tables, p.seq_lens, p.k_scale, p.v_scale, PL ? p.shared : nullptr);
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
@@ -917,11 +917,11 @@ int32_t launch_t(const DecodeParams& p, hipStream_t stream) {
   const dim3 grid(p.Hkv, p.B);
   ProfileScope prof("cf_decode_merge", stream);
   switch (p.G) {
-    case 1: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 1>), grid, dim3(256), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 2>), grid, dim3(256), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 4>), grid, dim3(256), 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 8>), grid, dim3(256), 0, stream, p); break;
-    case 16: hipLaunchKernelGGL((decode_merge_kernel<QT, D, 16>), grid, dim3(256), 0, stream, p); break;
+    case 1: CF_LAUNCH((decode_merge_kernel<QT, D, 1>), grid, dim3(256), 0, stream, p); break;
+    case 2: CF_LAUNCH((decode_merge_kernel<QT, D, 2>), grid, dim3(256), 0, stream, p); break;
+    case 4: CF_LAUNCH((decode_merge_kernel<QT, D, 4>), grid, dim3(256), 0, stream, p); break;
+    case 8: CF_LAUNCH((decode_merge_kernel<QT, D, 8>), grid, dim3(256), 0, stream, p); break;
+    case 16: CF_LAUNCH((decode_merge_kernel<QT, D, 16>), grid, dim3(256), 0, stream, p); break;
     default: set_error("MFMA decode: unsupported GQA group %d", p.G); return CF_ERR_UNSUPPORTED;
   }
   CF_HIP_CHECK(hipGetLastError());

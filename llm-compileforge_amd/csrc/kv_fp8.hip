@@ -412,7 +412,7 @@ int32_t launch_amax_scale(const Rank4& x, int x_dt, float* scales, int64_t s_str
   uint32_t* acc = (uint32_t*)scales;
   {
     ProfileScope prof("cf_fp8_zero", stream);
-    hipLaunchKernelGGL(zero_u32_kernel, dim3((H + 255) / 256), dim3(256), 0, stream, acc, H);
+    CF_LAUNCH(zero_u32_kernel, dim3((H + 255) / 256), dim3(256), 0, stream, acc, H);
   }
   CF_HIP_CHECK(hipGetLastError());
   const int64_t T = x.size[0] * x.size[1];
@@ -423,9 +423,9 @@ int32_t launch_amax_scale(const Rank4& x, int x_dt, float* scales, int64_t s_str
     const bool vec = rows_vectorizable(x, x_dt == kF32 ? 4 : 2);
     ProfileScope prof("cf_fp8_amax", stream);
     switch (x_dt) {
-      case kF32: hipLaunchKernelGGL((amax_rows_kernel<kF32>), grid, dim3(256), 0, stream, x, acc, rows, vec); break;
-      case kF16: hipLaunchKernelGGL((amax_rows_kernel<kF16>), grid, dim3(256), 0, stream, x, acc, rows, vec); break;
-      case kBF16: hipLaunchKernelGGL((amax_rows_kernel<kBF16>), grid, dim3(256), 0, stream, x, acc, rows, vec); break;
+      case kF32: CF_LAUNCH((amax_rows_kernel<kF32>), grid, dim3(256), 0, stream, x, acc, rows, vec); break;
+      case kF16: CF_LAUNCH((amax_rows_kernel<kF16>), grid, dim3(256), 0, stream, x, acc, rows, vec); break;
+      case kBF16: CF_LAUNCH((amax_rows_kernel<kBF16>), grid, dim3(256), 0, stream, x, acc, rows, vec); break;
       default: set_error("amax: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
     }
     CF_HIP_CHECK(hipGetLastError());
@@ -434,16 +434,16 @@ int32_t launch_amax_scale(const Rank4& x, int x_dt, float* scales, int64_t s_str
     const dim3 grid((unsigned)ceil_div(T, rows), H);
     ProfileScope prof("cf_fp8_amax", stream);
     switch (x_dt) {
-      case kF32: hipLaunchKernelGGL((amax_kernel<kF32>), grid, dim3(256), 0, stream, x, acc, rows); break;
-      case kF16: hipLaunchKernelGGL((amax_kernel<kF16>), grid, dim3(256), 0, stream, x, acc, rows); break;
-      case kBF16: hipLaunchKernelGGL((amax_kernel<kBF16>), grid, dim3(256), 0, stream, x, acc, rows); break;
+      case kF32: CF_LAUNCH((amax_kernel<kF32>), grid, dim3(256), 0, stream, x, acc, rows); break;
+      case kF16: CF_LAUNCH((amax_kernel<kF16>), grid, dim3(256), 0, stream, x, acc, rows); break;
+      case kBF16: CF_LAUNCH((amax_kernel<kBF16>), grid, dim3(256), 0, stream, x, acc, rows); break;
       default: set_error("amax: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
     }
     CF_HIP_CHECK(hipGetLastError());
   }
   {
     ProfileScope prof("cf_fp8_scale", stream);
-    hipLaunchKernelGGL(scale_from_amax_kernel, dim3((H + 255) / 256), dim3(256), 0, stream, acc, s_stride, H);
+    CF_LAUNCH(scale_from_amax_kernel, dim3((H + 255) / 256), dim3(256), 0, stream, acc, s_stride, H);
   }
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
@@ -458,9 +458,9 @@ int32_t launch_quantize(const Rank4& x, int x_dt, const float* scales, int64_t s
     const dim3 grid(grid_for(n / 16));
     const bool xv = rows_vectorizable(x, x_dt == kF32 ? 4 : 2), ov = rows_vectorizable(out, 1);
     switch (x_dt) {
-      case kF32: hipLaunchKernelGGL((quantize_rows_kernel<kF32>), grid, dim3(256), 0, stream, x, scales, s_stride, out, xv, ov); break;
-      case kF16: hipLaunchKernelGGL((quantize_rows_kernel<kF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out, xv, ov); break;
-      case kBF16: hipLaunchKernelGGL((quantize_rows_kernel<kBF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out, xv, ov); break;
+      case kF32: CF_LAUNCH((quantize_rows_kernel<kF32>), grid, dim3(256), 0, stream, x, scales, s_stride, out, xv, ov); break;
+      case kF16: CF_LAUNCH((quantize_rows_kernel<kF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out, xv, ov); break;
+      case kBF16: CF_LAUNCH((quantize_rows_kernel<kBF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out, xv, ov); break;
       default: set_error("quantize: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
     }
     CF_HIP_CHECK(hipGetLastError());
@@ -468,9 +468,9 @@ int32_t launch_quantize(const Rank4& x, int x_dt, const float* scales, int64_t s
   }
   const dim3 grid(grid_for(n));
   switch (x_dt) {
-    case kF32: hipLaunchKernelGGL((quantize_kernel<kF32>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
-    case kF16: hipLaunchKernelGGL((quantize_kernel<kF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
-    case kBF16: hipLaunchKernelGGL((quantize_kernel<kBF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
+    case kF32: CF_LAUNCH((quantize_kernel<kF32>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
+    case kF16: CF_LAUNCH((quantize_kernel<kF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
+    case kBF16: CF_LAUNCH((quantize_kernel<kBF16>), grid, dim3(256), 0, stream, x, scales, s_stride, out); break;
     default: set_error("quantize: unsupported dtype %d", x_dt); return CF_ERR_UNSUPPORTED;
   }
   CF_HIP_CHECK(hipGetLastError());
@@ -483,12 +483,12 @@ int32_t launch_dequantize(const Rank4& q, const float* scales, int64_t s_stride,
   if (n == 0) return CF_OK;
   ProfileScope prof("cf_fp8_dequantize", stream);
   if (q.size[3] % 16 == 0) {
-    hipLaunchKernelGGL(dequantize_rows_kernel, dim3(grid_for(n / 16)), dim3(256), 0, stream, q, scales, s_stride, out,
+    CF_LAUNCH(dequantize_rows_kernel, dim3(grid_for(n / 16)), dim3(256), 0, stream, q, scales, s_stride, out,
                        rows_vectorizable(q, 1), rows_vectorizable(out, 4));
     CF_HIP_CHECK(hipGetLastError());
     return CF_OK;
   }
-  hipLaunchKernelGGL(dequantize_kernel, dim3(grid_for(n)), dim3(256), 0, stream, q, scales, s_stride, out);
+  CF_LAUNCH(dequantize_kernel, dim3(grid_for(n)), dim3(256), 0, stream, q, scales, s_stride, out);
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
 }
@@ -503,7 +503,7 @@ int32_t launch_kv_write_fp8(const KvWriteParams& p, int x_dt, int slot_dt, hipSt
     const dim3 grid((unsigned)blocks);
     ProfileScope prof("cf_kv_write_fp8", stream);
 #define CF_KVN(XT, ST) \
-  hipLaunchKernelGGL((kv_write_native_kernel<XT, ST>), grid, dim3(256), 0, stream, p, k_blocks, v_chunks)
+  CF_LAUNCH((kv_write_native_kernel<XT, ST>), grid, dim3(256), 0, stream, p, k_blocks, v_chunks)
     switch (x_dt * 8 + (slot_dt == kI64 ? 1 : 0)) {
       case kF32 * 8: CF_KVN(kF32, kI32); break;
       case kF32 * 8 + 1: CF_KVN(kF32, kI64); break;
@@ -520,7 +520,7 @@ int32_t launch_kv_write_fp8(const KvWriteParams& p, int x_dt, int slot_dt, hipSt
   const dim3 grid((unsigned)p.T);
   const int threads = p.H * p.D >= 256 ? 256 : 64 * (int)ceil_div(p.H * p.D, 64);
   ProfileScope prof("cf_kv_write_fp8", stream);
-#define CF_KVW(XT, ST) hipLaunchKernelGGL((kv_write_kernel<XT, ST>), grid, dim3(threads), 0, stream, p)
+#define CF_KVW(XT, ST) CF_LAUNCH((kv_write_kernel<XT, ST>), grid, dim3(threads), 0, stream, p)
   if (slot_dt == kI64) {
     switch (x_dt) {
       case kF32: CF_KVW(kF32, kI64); break;

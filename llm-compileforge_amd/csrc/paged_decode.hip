@@ -267,10 +267,10 @@ int32_t launch_generic_t(const DecodeParams& p, hipStream_t stream) {
   }
   if (p.max_parts == 1) {
     ProfileScope prof("cf_decode_generic", stream);
-    hipLaunchKernelGGL((decode_generic_kernel<QT, KT, true>), grid, dim3(kGenericThreads), lds, stream, p);
+    CF_LAUNCH((decode_generic_kernel<QT, KT, true>), grid, dim3(kGenericThreads), lds, stream, p);
   } else {
     ProfileScope prof("cf_decode_generic", stream);
-    hipLaunchKernelGGL((decode_generic_kernel<QT, KT, false>), grid, dim3(kGenericThreads), lds, stream, p);
+    CF_LAUNCH((decode_generic_kernel<QT, KT, false>), grid, dim3(kGenericThreads), lds, stream, p);
   }
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
@@ -310,9 +310,9 @@ int32_t launch_decode_reduce(const DecodeParams& p, int q_dt, hipStream_t stream
   const int threads = 256;
   ProfileScope prof("cf_decode_reduce", stream);
   switch (q_dt) {
-    case kF32: hipLaunchKernelGGL((decode_reduce_kernel<kF32>), grid, dim3(threads), 0, stream, p); break;
-    case kF16: hipLaunchKernelGGL((decode_reduce_kernel<kF16>), grid, dim3(threads), 0, stream, p); break;
-    case kBF16: hipLaunchKernelGGL((decode_reduce_kernel<kBF16>), grid, dim3(threads), 0, stream, p); break;
+    case kF32: CF_LAUNCH((decode_reduce_kernel<kF32>), grid, dim3(threads), 0, stream, p); break;
+    case kF16: CF_LAUNCH((decode_reduce_kernel<kF16>), grid, dim3(threads), 0, stream, p); break;
+    case kBF16: CF_LAUNCH((decode_reduce_kernel<kBF16>), grid, dim3(threads), 0, stream, p); break;
     default: set_error("unsupported output dtype %d", q_dt); return CF_ERR_UNSUPPORTED;
   }
   CF_HIP_CHECK(hipGetLastError());

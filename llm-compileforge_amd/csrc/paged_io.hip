@@ -168,7 +168,7 @@ int32_t launch_paged_write(const PagedWriteParams& p, int x_dt, int slot_dt, int
   const dim3 grid((unsigned)grid_of(threads));
   ProfileScope prof("cf_paged_write", stream);
 #define CF_PW(XT, ST, CT) \
-  hipLaunchKernelGGL((paged_write_kernel<XT, ST, CT>), grid, dim3(256), 0, stream, p, pw, xvec, cvec)
+  CF_LAUNCH((paged_write_kernel<XT, ST, CT>), grid, dim3(256), 0, stream, p, pw, xvec, cvec)
 #define CF_PW_C(XT, ST)                                                              \
   switch (cache_dt) {                                                                \
     case kF32: CF_PW(XT, ST, kF32); break;                                           \
@@ -206,7 +206,7 @@ int32_t launch_paged_gather(const PagedGatherParams& p, int cache_dt, int out_dt
   const dim3 grid((unsigned)grid_of(threads));
   ProfileScope prof("cf_paged_gather", stream);
 #define CF_PG(CT, OT) \
-  hipLaunchKernelGGL((paged_gather_kernel<CT, OT>), grid, dim3(256), 0, stream, p, pw, cvec, ovec)
+  CF_LAUNCH((paged_gather_kernel<CT, OT>), grid, dim3(256), 0, stream, p, pw, cvec, ovec)
 #define CF_PG_O(CT)                                                                  \
   switch (out_dt) {                                                                  \
     case kF32: CF_PG(CT, kF32); break;                                               \

@@ -526,12 +526,12 @@ int32_t launch_t(PrefillParams& p, hipStream_t stream) {
   }
   {
     ProfileScope prof("cf_prefill_plan", stream);
-    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
+    CF_LAUNCH(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
   }
   CF_HIP_CHECK(hipGetLastError());
   {
     ProfileScope prof("cf_prefill_mfma", stream);
-    hipLaunchKernelGGL((prefill_item_kernel<KT, D, G>), dim3(prefill_cus() * per_cu), dim3(256), 0, stream, p,
+    CF_LAUNCH((prefill_item_kernel<KT, D, G>), dim3(prefill_cus() * per_cu), dim3(256), 0, stream, p,
                        p.tables, (const int4*)p.items, (const int4*)p.chunks, p.header, p.k_scale, p.v_scale);
   }
   CF_HIP_CHECK(hipGetLastError());

@@ -4,7 +4,8 @@ Tolerances: fp32 max-abs 1e-5; bf16 and fp8
 max-abs 2e-2 with cosine >= 0.9999.  Small and mid sizes compare with the
 float64 oracle directly; full benchmark sizes use size-independent
 properties (block-permutation invariance, shared prefix == copied prefix,
-split-KV == no split) plus an oracle check on a sample of sequences.
+rerun and grouped/ungrouped agreement) plus an oracle check on a sample of
+sequences that includes the longest one.
 """
 
 from __future__ import annotations
@@ -18,7 +19,7 @@ import torch
 from cf_hip import layout as L
 from cf_hip import ops, workloads
 from kernels.paged_attention import paged_attention, paged_attention_tensors
-from tests.gpu_util import assert_close, metrics, oracle_decode
+from tests.gpu_util import assert_close, oracle_decode
 
 pytestmark = pytest.mark.gpu
 
@@ -44,14 +45,24 @@ def test_configs_match_oracle(gpu, config, batch, layout):
     assert_close(out.float().cpu().numpy(), ref, case.q.dtype, f"{config}/{layout}")
 
 
-@pytest.mark.parametrize("pt", [16, 64, 256, 1024])
+@pytest.mark.parametrize("pt", [16, 48, 64, 256])
 def test_partition_sizes_agree(gpu, pt):
-    print(f"[case] c2 partitions={pt}", flush=True)
-    case = workloads.make_case("c2_tinyllama", device=gpu, seed=3, batch=8)
+    """Split-KV partition sizes on the generic (partitioned) path: fp32
+    caches only run there, so every size really changes the split (at the
+    full c2 batch the launch holds >= 1024 workgroups from 256-token
+    partitions down, so none of these is shortened), and the log-sum-exp
+    reduce runs."""
+    print(f"[case] c2 shape, fp32 caches, partitions={pt}", flush=True)
+    case = workloads.make_case("c2_tinyllama", device=gpu, seed=3)
+    case.q = case.q.float()
+    case.kv_dtype = torch.float32
     kc, vc, ks, vs = workloads.materialize(case, "native")
-    out = _run(case, kc, vc, ks, vs, gpu, pt=pt)
+    with ops.KernelTimer() as timer:
+        out = _run(case, kc, vc, ks, vs, gpu, pt=pt)
+        assert timer.query("cf_decode_generic")[1] == 1 and timer.query("cf_decode_mfma")[1] == 0
+        assert timer.query("cf_decode_reduce")[1] == 1
     ref = oracle_decode(case, kc, vc, ks, vs)
-    assert_close(out.float().cpu().numpy(), ref, case.q.dtype, f"pt={pt}")
+    assert_close(out.float().cpu().numpy(), ref, torch.float32, f"pt={pt}")
 
 
 @pytest.mark.parametrize("hq,hkv,d,bs", [(8, 8, 64, 16), (8, 2, 128, 16), (16, 1, 64, 16), (32, 2, 128, 16),
@@ -183,9 +194,9 @@ def test_dict_api_back_to_back_calls(gpu):
 
 
 def test_full_c3_properties(gpu):
-    """Full headline config: block-permutation invariance (bitwise), shared
-    prefix == copied prefix (bitwise), split-KV sizes agree, and the oracle
-    on a sample of sequences."""
+    """Full headline config, native layout, no shared-prefix statement:
+    block-permutation invariance (bitwise), shared prefix == copied prefix
+    (bitwise), and the oracle on a sample of sequences."""
     print("[case] c3 full size", flush=True)
     case = workloads.make_case("c3_llama3_8b", device=gpu, seed=0)
     kc, vc, ks, vs = workloads.materialize(case, "native")
@@ -216,12 +227,7 @@ def test_full_c3_properties(gpu):
     out3 = _run(case, kc3, vc3, ks, vs, gpu, tables=t3)
     assert torch.equal(out, out3)
     del kc3, vc3
-    # 3. partition sizes
-    for pt in (256, 1024, 2048):
-        o = _run(case, kc, vc, ks, vs, gpu, pt=pt)
-        err, cos = metrics(o.float().cpu().numpy(), out.float().cpu().numpy())
-        assert err < 2e-2 and cos > 0.9999, (pt, err, cos)
-    # 4. oracle on a sample of sequences (shared and private)
+    # 3. oracle on a sample of sequences (shared and private)
     idx = [0, 1, 31, 32, 63]
     sub = workloads.DecodeCase("c3_sample", case.q[idx], case.k, case.v, [case.block_tables[i] for i in idx],
                                [case.seq_lens[i] for i in idx], 16, case.scale, case.kv_dtype)
@@ -361,3 +367,91 @@ def test_softmax_scales(gpu, scale, kv_dtype):
     out = _run(case, kc, vc, ks, vs, gpu)
     ref = oracle_decode(case, kc, vc, ks, vs)
     assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, f"decode scale {scale} {kv_dtype}")
+
+
+def _sample_ids(lens: list[int], fixed: list[int], n_random: int, seed: int) -> list[int]:
+    """`fixed` ids, the longest and shortest sequence, and n_random more."""
+    rng = np.random.default_rng(seed)
+    ids = set(i for i in fixed if i < len(lens))
+    ids.add(int(np.argmax(lens)))
+    ids.add(int(np.argmin(lens)))
+    rest = [i for i in range(len(lens)) if i not in ids]
+    ids.update(int(i) for i in rng.choice(rest, size=min(n_random, len(rest)), replace=False))
+    return sorted(ids)
+
+
+def _permuted_paired(kc, vc, gpu, seed: int):
+    """The same cache contents under a seeded permutation of the physical
+    block ids: (k, v, inverse map old id -> new id)."""
+    nb, bs, hkv, d = kc.shape
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed)).to(gpu)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(nb, device=gpu)
+    k2, v2 = L.alloc_kv_cache(nb, bs, hkv, d, kc.dtype, gpu, "paired")
+    k2.copy_(kc[perm])
+    v2.copy_(vc[perm])
+    return k2, v2, inv
+
+
+def test_full_c3_as_benchmarked(gpu):
+    """BASELINE configs[2] exactly as bench.py times it: batch 64, paired KV
+    layout, the shared-prefix statement, a DecodePlan rerun step after step.
+    Oracle on 20 sequences (sharers at group edges, private ones, the
+    longest and the shortest); reruns bitwise identical; block-permutation
+    invariance (bitwise) over the whole batch."""
+    print("[case] c3 full size, paired layout, shared-prefix statement (the benchmark step)", flush=True)
+    case = workloads.make_case("c3_llama3_8b", device=gpu, seed=0)
+    kc, vc, ks, vs = workloads.materialize(case, "paired")
+    assert L.layout_of(kc, False) == "paired" and L.layout_of(vc, True) == "paired"
+    tables, lens = case.tables_tensor(gpu), case.seq_lens_tensor(gpu)
+    shared_list = ops.shared_prefix_lens(case.block_tables, case.seq_lens, 16)
+    assert shared_list[1:32] == [1024] * 31 and not any(shared_list[32:])
+    shared = torch.tensor(shared_list, dtype=torch.int32, device=gpu)
+    plan = ops.DecodePlan(case.q, kc, vc, tables, lens, case.scale, 16, ks, vs, shared_prefix_lens=shared)
+    with ops.KernelTimer() as timer:
+        out = plan.run().clone()
+        torch.cuda.synchronize()
+        assert timer.query("cf_decode_mfma")[1] == 1 and timer.query("cf_decode_generic")[1] == 0
+    for _ in range(3):
+        again = plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(again, out)
+    idx = _sample_ids(case.seq_lens, [0, 1, 3, 4, 7, 8, 15, 16, 30, 31, 32, 33, 62, 63], 4, seed=1)
+    assert len(idx) >= 16
+    sub = workloads.DecodeCase("c3_sample", case.q[idx], case.k, case.v, [case.block_tables[i] for i in idx],
+                               [case.seq_lens[i] for i in idx], 16, case.scale, case.kv_dtype)
+    ref = oracle_decode(sub, kc, vc, ks, vs)
+    assert_close(out[idx].float().cpu().numpy(), ref, torch.bfloat16, f"c3 benchmarked step, {len(idx)} sequences")
+    k2, v2, inv = _permuted_paired(kc, vc, gpu, seed=5)
+    t2 = inv[tables.long()].to(torch.int32)
+    out2 = ops.DecodePlan(case.q, k2, v2, t2, lens, case.scale, 16, ks, vs, shared_prefix_lens=shared).run()
+    torch.cuda.synchronize()
+    assert torch.equal(out2, out)
+
+
+def test_full_c4_llama3_70b(gpu):
+    """BASELINE configs[3] at full size: batch 128, 64 query / 8 KV heads,
+    lognormal contexts up to 32,768 tokens, paired layout.  Oracle on 16
+    sequences including the longest; block-permutation invariance
+    (bitwise) over the whole batch; a second call bitwise identical."""
+    print("[case] c4 full size (batch 128), paired layout", flush=True)
+    case = workloads.make_case("c4_llama3_70b", device=gpu, seed=0)
+    assert case.batch == 128 and case.q.shape[1] == 64 and case.num_kv_heads == 8
+    kc, vc, ks, vs = workloads.materialize(case, "paired")
+    tables, lens = case.tables_tensor(gpu), case.seq_lens_tensor(gpu)
+    with ops.KernelTimer() as timer:
+        out = _run(case, kc, vc, ks, vs, gpu)
+        assert timer.query("cf_decode_mfma")[1] == 1
+    again = _run(case, kc, vc, ks, vs, gpu)
+    assert torch.equal(again, out)
+    order = np.argsort(case.seq_lens)
+    idx = _sample_ids(case.seq_lens, [0, 1, 64, 127, int(order[-2]), int(order[-3])], 10, seed=2)
+    assert len(idx) >= 16 and int(np.argmax(case.seq_lens)) in idx
+    print(f"[case] c4 oracle on {len(idx)} sequences, longest {max(case.seq_lens)} tokens", flush=True)
+    sub = workloads.DecodeCase("c4_sample", case.q[idx], case.k, case.v, [case.block_tables[i] for i in idx],
+                               [case.seq_lens[i] for i in idx], 16, case.scale, case.kv_dtype)
+    ref = oracle_decode(sub, kc, vc, ks, vs)
+    assert_close(out[idx].float().cpu().numpy(), ref, torch.bfloat16, f"c4 full, {len(idx)} sequences")
+    k2, v2, inv = _permuted_paired(kc, vc, gpu, seed=6)
+    out2 = _run(case, k2, v2, ks, vs, gpu, tables=inv[tables.long()].to(torch.int32))
+    assert torch.equal(out2, out)

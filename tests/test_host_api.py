@@ -95,6 +95,31 @@ def test_hip_backend_dispatch_and_errors():
                                   torch.zeros(1, 1, dtype=torch.int32)])
 
 
+def test_hip_backend_sdpa_routing_on_the_host():
+    """scaled_dot_product_attention takes 3-4 inputs (the reference's
+    registration); calls the HIP kernels do not run -- CPU tensors, a mask,
+    dropout, a query longer than one token, head counts torch would reject --
+    go to the fallback with their inputs and kwargs unchanged, and without a
+    fallback raise ValueError."""
+    fb = _Recorder()
+    be = HipBackend(fallback=fb)
+    q, k, v = torch.zeros(2, 4, 1, 8), torch.zeros(2, 4, 5, 8), torch.zeros(2, 4, 5, 8)
+    mask = torch.zeros(2, 1, 1, 5)
+    be.execute("scaled_dot_product_attention", [q, k, v])
+    be.execute("scaled_dot_product_attention", [q, k, v, mask], is_causal=False)
+    be.execute("scaled_dot_product_attention", [torch.zeros(2, 4, 3, 8), k, v], scale=0.5)
+    assert fb.calls == [("scaled_dot_product_attention", 3, {}),
+                        ("scaled_dot_product_attention", 4, {"is_causal": False}),
+                        ("scaled_dot_product_attention", 3, {"scale": 0.5})]
+    with pytest.raises(ValueError, match="at least 3"):
+        be.execute("scaled_dot_product_attention", [q, k])
+    with pytest.raises(ValueError, match="at most 4"):
+        be.execute("scaled_dot_product_attention", [q, k, v, mask, mask])
+    with pytest.raises(ValueError, match="no fallback"):
+        HipBackend().execute("scaled_dot_product_attention", [q, k, v])
+    assert "scaled_dot_product_attention" in HipBackend.supported_ops()
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
 def test_layouts(dtype):
     k, v = L.alloc_kv_cache(5, 16, 4, 32, dtype, "cpu", "native")
