@@ -150,6 +150,31 @@ int32_t cf_paged_decode_shared(const CfTensor* q, const CfTensor* k_cache,
                                void* workspace, uint64_t workspace_bytes,
                                void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops or harnesses
+ * that forbid hipMalloc): cf_paged_decode_shared with the workspace taken
+ * from a fixed scratch array inside the library instead of a caller
+ * buffer -- 64 MiB (67,108,864 bytes) per device, held by every GPU the
+ * library runs on until the process ends.  Same arguments, results and
+ * errors as cf_paged_decode_shared minus the workspace; the caller still
+ * passes every input and the output.  A call whose workspace need
+ * (cf_paged_decode_workspace_bytes) exceeds the scratch returns
+ * CF_ERR_WORKSPACE with the need in the message (the Llama-3-70B shape at
+ * batch 128 needs about 26 MB).  Allocates nothing: no hipMalloc, no
+ * hipFree.  All calls on one device share its scratch and leave their
+ * contents there, so calls that overlap on one device -- on two streams,
+ * or from two threads without ordering -- race. */
+int32_t cf_paged_decode_shared_noalloc(const CfTensor* q, const CfTensor* k_cache,
+                                       const CfTensor* v_cache,
+                                       const CfTensor* block_tables,
+                                       const CfTensor* seq_lens,
+                                       const CfTensor* shared_prefix_lens,
+                                       const CfTensor* k_scale,
+                                       const CfTensor* v_scale, float scale,
+                                       int32_t block_size,
+                                       int32_t partition_tokens, CfTensor* out,
+                                       void* stream);
+
 /* Workspace needed by cf_prefill_chunk_fp8 (on the current device) for
  * num_q_tokens query rows in num_chunks chunks.  Grows with the query
  * rows (one small record per query block), not with the cached context. */

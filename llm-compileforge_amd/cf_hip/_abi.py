@@ -147,6 +147,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_float, ctypes.c_int32, ctypes.c_int32, _P, ctypes.c_void_p,
          ctypes.c_uint64, ctypes.c_void_p],
     ),
+    "cf_paged_decode_shared_noalloc": (
+        ctypes.c_int32,
+        [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_float, ctypes.c_int32, ctypes.c_int32, _P, ctypes.c_void_p],
+    ),
     "cf_prefill_chunk_workspace_bytes": (
         ctypes.c_int32,
         [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,

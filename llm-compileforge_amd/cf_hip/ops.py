@@ -161,6 +161,52 @@ def paged_decode(
     return out
 
 
+NOALLOC_SCRATCH_BYTES = 64 << 20  # the library's fixed per-device scratch (cf_paged_decode_shared_noalloc)
+
+
+def paged_decode_noalloc(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    partition_tokens: int = DEFAULT_PARTITION_TOKENS,
+    out: torch.Tensor | None = None,
+    shared_prefix_lens: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """paged_decode for callers that cannot allocate: the library's fixed
+    per-device scratch replaces the workspace, so the call itself allocates
+    nothing (pass `out` to keep torch from allocating the output).  Calls
+    that overlap on one device race on that scratch; a call needing more
+    than NOALLOC_SCRATCH_BYTES raises ValueError."""
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("block_tables", block_tables),
+                    ("seq_lens", seq_lens)):
+        _require_device(name, t)
+    dev = _same_device(q, k_cache, v_cache, block_tables, seq_lens)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=dev)
+    ks = descriptor(k_scale) if k_scale is not None else None
+    vs = descriptor(v_scale) if v_scale is not None else None
+    dsh = None
+    if shared_prefix_lens is not None:
+        _require_device("shared_prefix_lens", shared_prefix_lens)
+        _same_device(q, shared_prefix_lens)
+        dsh = descriptor(shared_prefix_lens)
+    dq, dk, dv = descriptor(q), descriptor(k_cache), descriptor(v_cache)
+    dt, dsl, do = descriptor(block_tables), descriptor(seq_lens), descriptor(out)
+    with _on(dev):
+        rc = lib().cf_paged_decode_shared_noalloc(
+            ref(dq), ref(dk), ref(dv), ref(dt), ref(dsl), ref(dsh), ref(ks), ref(vs),
+            float(scale), int(block_size), int(partition_tokens), ref(do), stream_handle(dev),
+        )
+    check(rc, "cf_paged_decode_shared_noalloc")
+    return out
+
+
 def prefill_workspace_bytes(num_q_tokens: int, num_chunks: int, num_q_heads: int, num_kv_heads: int,
                             head_dim: int, block_size: int = 16) -> int:
     out = ctypes.c_uint64(0)
@@ -512,6 +558,7 @@ class KernelTimer:
 
 __all__ = [
     "DEFAULT_PARTITION_TOKENS",
+    "NOALLOC_SCRATCH_BYTES",
     "DecodePlan",
     "KernelTimer",
     "block_span_view",
@@ -527,6 +574,7 @@ __all__ = [
     "fp8_quantize",
     "kv_write_fp8",
     "paged_decode",
+    "paged_decode_noalloc",
     "paged_gather",
     "paged_write",
     "shared_prefix_lens",

@@ -181,6 +181,40 @@ int32_t view_of_34(const CfTensor* t, const char* name, View* v) {
 }
 }  // namespace
 
+// ---- fixed scratch for the no-allocation decode entry point -------------
+// Device memory the library owns for callers that cannot allocate: one
+// array per device, held from the code object's load until the process
+// ends.  Host code never uses the array's name as an address (in host code
+// it is only a stand-in); the device address comes from hipGetSymbolAddress
+// once per device, with that device current, and is kept per device.
+constexpr uint64_t kNoAllocScratchBytes = 64ull << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// The current device's scratch address (resolved on its first use there).
+int32_t noalloc_scratch(void** out) {
+  int dev = -1;
+  CF_HIP_CHECK(hipGetDevice(&dev));
+  CF_CHECK(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+      return CF_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return CF_OK;
+}
+
 }  // namespace cf
 
 using namespace cf;
@@ -382,6 +416,27 @@ int32_t cf_paged_decode_shared(const CfTensor* q, const CfTensor* k_cache, const
   rc = launch_decode_generic(p, vq.dtype, vk.dtype, st);
   if (rc) return rc;
   if (p.max_parts > 1) rc = launch_decode_reduce(p, vq.dtype, st);
+  return rc;
+}
+
+int32_t cf_paged_decode_shared_noalloc(const CfTensor* q, const CfTensor* k_cache, const CfTensor* v_cache,
+                                       const CfTensor* block_tables, const CfTensor* seq_lens,
+                                       const CfTensor* shared_prefix_lens, const CfTensor* k_scale,
+                                       const CfTensor* v_scale, float scale, int32_t block_size,
+                                       int32_t partition_tokens, CfTensor* out, void* stream) {
+  void* ws = nullptr;
+  int32_t rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  // The decode kernels rewrite every workspace cell they read in the same
+  // call (merge descriptors, partial rows), so nothing needs clearing.
+  rc = cf_paged_decode_shared(q, k_cache, v_cache, block_tables, seq_lens, shared_prefix_lens, k_scale, v_scale,
+                              scale, block_size, partition_tokens, out, ws, kNoAllocScratchBytes, stream);
+  if (rc == CF_ERR_WORKSPACE) {
+    const std::string msg = last_error();
+    set_error("this call needs more than the library's fixed scratch of %llu bytes per device (%s); use "
+              "cf_paged_decode_shared with a workspace",
+              (unsigned long long)kNoAllocScratchBytes, msg.c_str());
+  }
   return rc;
 }
 
