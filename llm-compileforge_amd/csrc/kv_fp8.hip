@@ -397,6 +397,142 @@ bool rows_vectorizable(const Rank4& v, int eb) {
   return true;
 }
 
+// ---- span kernels (32-bit indexing) ---------------------------------------
+// For views whose rows are uniformly strided ([S0, S1] folds into one row
+// axis) and whose 16-element pieces are contiguous and 16-byte aligned.
+// Piece k of a launch is (row k / P, head (k % P) / np, piece (k % P) % np)
+// with np = D / 16 and P = H * np, so consecutive threads read consecutive
+// pieces of a row; the host checks that rows * P fits in 31 bits.
+struct SpanView {
+  const char* base;    // bytes
+  int64_t row_stride;  // bytes
+  int64_t head_stride; // bytes
+  int rows, H, np, P;
+};
+
+constexpr int kSpanMaxHeads = 1024;  // per-head maxima a workgroup keeps in LDS
+
+// amax over a span: each workgroup takes a contiguous range of rows, keeps
+// one running max per head in LDS (a thread flushes its register max when
+// its piece moves to another head), then raises the global per-head bits
+// with atomicMax only where its max exceeds the value already there -- so
+// after the first few workgroups almost none of them issue the atomic, and
+// the launch can be wide without the workgroups queueing on H addresses.
+template <int XT>
+__global__ __launch_bounds__(256) void amax_span_kernel(SpanView v, uint32_t* amax_bits, int rows_per_wg, int q256,
+                                                        int r256) {
+  constexpr int EB = sizeof(typename Elem<XT>::T);
+  __shared__ uint32_t hmax[kSpanMaxHeads];
+  for (int h = threadIdx.x; h < v.H; h += 256) hmax[h] = 0u;
+  __syncthreads();
+  const int r_begin = blockIdx.x * rows_per_wg;
+  const int r_end = min(r_begin + rows_per_wg, v.rows);
+  const int n = (r_end - r_begin) * v.P;
+  int row = r_begin + (int)threadIdx.x / v.P, rem = (int)threadIdx.x % v.P;
+  int cur = -1;
+  uint32_t m = 0u;
+  for (int k = threadIdx.x; k < n; k += 256) {
+    const int h = rem / v.np, c = rem - h * v.np;
+    float f[16];
+    load16<XT>(v.base + row * v.row_stride + h * v.head_stride + c * 16 * EB, f);
+    if (h != cur) {
+      if (cur >= 0 && m != 0u) atomicMax(&hmax[cur], m);
+      cur = h;
+      m = 0u;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t u = f2u(f[e]) & 0x7FFFFFFFu;
+      m = m > u ? m : u;
+    }
+    row += q256;
+    rem += r256;
+    if (rem >= v.P) {
+      rem -= v.P;
+      ++row;
+    }
+  }
+  if (cur >= 0 && m != 0u) atomicMax(&hmax[cur], m);
+  __syncthreads();
+  for (int h = threadIdx.x; h < v.H; h += 256) {
+    const uint32_t mine = hmax[h];
+    if (mine != 0u && mine > __hip_atomic_load(amax_bits + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      atomicMax(amax_bits + h, mine);
+  }
+}
+
+// One thread per piece of a span: 16 elements in, one 16-byte store out
+// (token-major outputs, e.g. the native / paired K tile rows).
+template <int XT>
+__global__ __launch_bounds__(256) void quantize_span_kernel(SpanView x, const float* scales, int64_t s_stride,
+                                                            char* out, int64_t o_row, int64_t o_head, int n) {
+  constexpr int EB = sizeof(typename Elem<XT>::T);
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= n) return;
+  const int row = k / x.P, rem = k - row * x.P;
+  const int h = rem / x.np, c = rem - h * x.np;
+  float f[16];
+  load16<XT>(x.base + row * x.row_stride + h * x.head_stride + c * 16 * EB, f);
+  const float sc = scales[h * s_stride];
+  uint32_t b[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) b[e] = e4m3_from_f32(f[e] / sc);
+  *(uint4*)(out + row * o_row + h * o_head + c * 16) = pack16(b);
+}
+
+// Channel-major outputs with 16 tokens per block (the native / paired V
+// tile: the 16 tokens of one channel are 16 contiguous bytes).  One thread
+// per (block, head, channel): the channel's 16 tokens are read from the
+// token-major source (consecutive threads read consecutive channels, so
+// every load instruction is one contiguous run), converted and written as
+// one 16-byte store -- the transpose happens in registers.
+template <int XT>
+__global__ __launch_bounds__(256) void quantize_transpose16_kernel(Rank4 x, const float* scales, int64_t s_stride,
+                                                                   char* out, int64_t o_blk, int64_t o_head,
+                                                                   int64_t o_chan, int n) {
+  using XE = Elem<XT>;
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= n) return;
+  const int D = (int)x.size[3], H = (int)x.size[2];
+  const int d = k % D;
+  const int hk = k / D;
+  const int h = hk % H;
+  const int a = hk / H;
+  const typename XE::T* src =
+      (const typename XE::T*)x.base + a * x.stride[0] + h * x.stride[2] + (int64_t)d * x.stride[3];
+  float f[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) f[t] = XE::load(src + t * x.stride[1]);
+  const float sc = scales[h * s_stride];
+  uint32_t b[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) b[t] = e4m3_from_f32(f[t] / sc);
+  *(uint4*)(out + a * o_blk + h * o_head + (int64_t)d * o_chan) = pack16(b);
+}
+
+// A SpanView of v (element size eb) when its rows fold into one uniformly
+// strided axis, its pieces are contiguous and 16-byte aligned and the launch
+// indexes fit in 31 bits.
+bool span_of(const Rank4& v, int eb, SpanView* s) {
+  if (v.size[3] % 16 != 0 || v.size[3] == 0 || v.stride[3] != 1 || ((uintptr_t)v.base & 15)) return false;
+  const int64_t rows = v.size[0] * v.size[1];
+  int64_t rs = v.stride[1];
+  if (v.size[1] == 1) rs = v.stride[0];
+  else if (v.size[0] > 1 && v.stride[0] != v.size[1] * v.stride[1]) return false;
+  if (((rs * eb) & 15) || ((v.stride[2] * eb) & 15)) return false;
+  if (v.size[2] > kSpanMaxHeads) return false;
+  const int64_t np = v.size[3] / 16, P = v.size[2] * np;
+  if (rows <= 0 || P <= 0 || rows * P >= (int64_t)INT32_MAX - 256) return false;
+  s->base = (const char*)v.base;
+  s->row_stride = rs * eb;
+  s->head_stride = v.stride[2] * eb;
+  s->rows = (int)rows;
+  s->H = (int)v.size[2];
+  s->np = (int)np;
+  s->P = (int)P;
+  return true;
+}
+
 int grid_for(int64_t n) {
   int64_t g = (n + 255) / 256;
   if (g > 65536) g = 65536;
