@@ -363,6 +363,79 @@ def bench_block_tables(args) -> dict:
     }
 
 
+def bench_fp8(args) -> dict:
+    """FP8 quantization kernels at the c3 pool size: per-KV-head amax ->
+    scale (reads the bf16 pool), quantize into the paired layout (K tiles
+    token-major, V tiles channel-major), each over K and V; plus the c5
+    step's paged FP8 write of 4344 new rows.  Durations from launch-stamped
+    HIP events; GB/s = algorithmic bytes (elements read + codes written)
+    / duration."""
+    import torch
+
+    from cf_hip import layout as L
+    from cf_hip import ops, workloads
+
+    dev = torch.device("cuda:0")
+    case = workloads.make_case("c3_llama3_8b", device=dev, seed=0)
+    nb, bs, hkv, d = case.k.shape
+    n = case.k.numel()
+    kc, vc = L.alloc_kv_cache(nb, bs, hkv, d, torch.float8_e4m3fn, dev, "paired")
+    ks = torch.empty(hkv, dtype=torch.float32, device=dev)
+    vs = torch.empty(hkv, dtype=torch.float32, device=dev)
+    mixed = workloads.make_mixed_case("c5_mixed", device=dev, seed=0)
+    t = workloads.materialize_mixed(mixed, "paired")
+
+    def step():
+        ops.fp8_amax_scale(case.k, out=ks)
+        ops.fp8_amax_scale(case.v, out=vs)
+        ops.fp8_quantize(case.k, ks, out=kc)
+        ops.fp8_quantize(case.v, vs, out=vc)
+        ops.kv_write_fp8(t["k_new"], t["v_new"], t["slots"], t["k_cache"], t["v_cache"], t["k_scale"], t["v_scale"])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = ops.KernelTimer()
+    with timer:
+        step()
+        torch.cuda.synchronize()
+        timer.reset()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    res = {}
+    src_bytes = n * case.k.element_size()
+    rows_new = t["k_new"].shape[0] * t["k_new"].shape[1] * t["k_new"].shape[2]
+    work = {
+        "cf_fp8_amax": ("amax -> scale over a bf16 [NB, 16, 8, 128] pool (K or V)", src_bytes, 2),
+        "cf_fp8_quantize": ("quantize a bf16 pool into the paired e4m3 layout (K or V)", src_bytes + n, 2),
+        "cf_kv_write_fp8": ("paged FP8 write of the c5 step's new K and V rows",
+                            2 * rows_new * t["k_new"].element_size() + 2 * rows_new, 1),
+    }
+    for name, (what, nbytes, per_step) in work.items():
+        ms, cnt = timer.query(name)
+        assert cnt == per_step * args.steps, (name, cnt)
+        us = ms / cnt * 1e3
+        res[name] = {"what": what, "us": us, "bytes": nbytes, "gbs": nbytes / (us / 1e6) / 1e9,
+                     "frac": nbytes / (us / 1e6) / 1e9 / HBM_PEAK_GBS}
+        log(f"{name}: {us:.1f} us, {res[name]['gbs']:.0f} GB/s ({res[name]['frac'] * 100:.1f} % of 8 TB/s)")
+    timer.reset()
+    q = res["cf_fp8_quantize"]
+    return {
+        "metric": "FP8 KV quantize GB/s (% of HBM peak), Llama-3-8B-shaped pool, 1 MI355X",
+        "value": q["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 -> e4m3", "data": "synthetic (seeded)",
+        "config": {"workload": "fp8_quantize", "pool": [nb, bs, hkv, d], "kv_layout": "paired",
+                   "write_rows": int(t["k_new"].shape[0]), "parallelism": "single GPU"},
+        "kernels": res,
+        "roofline": {"bound": "hbm", "kernel": "cf_fp8_quantize", "achieved": q["gbs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": q["frac"], "traffic": None},
+    }
+
+
 def bench_copy(args) -> dict:
     """A plain device copy of 1 GiB (torch's copy kernel), K times: the
     known-size reference the FETCH_SIZE / WRITE_SIZE counters are scaled by
@@ -427,6 +500,10 @@ def main() -> None:
         return
     if args.config == "block_tables":
         result = bench_block_tables(args)
+        print(json.dumps(result), flush=True)
+        return
+    if args.config == "fp8_quantize":
+        result = bench_fp8(args)
         print(json.dumps(result), flush=True)
         return
     if args.config == "copy_1gib":

@@ -181,6 +181,18 @@ int32_t view_of_34(const CfTensor* t, const char* name, View* v) {
 }
 }  // namespace
 
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // ---- fixed scratch for the no-allocation decode entry point -------------
 // Device memory the library owns for callers that cannot allocate: one
 // array per device, held from the code object's load until the process

@@ -42,6 +42,74 @@ __device__ __forceinline__ uint8_t e4m3_from_f32(float f) {
   return (uint8_t)(code | (sign >> 24));
 }
 
+// e4m3fn(x / scale) with x / scale correctly rounded in fp32 (the
+// reference's `(x.float() / scale).to(float8_e4m3fn)`), fast:
+//
+// 1. The quotient is computed as x * (1 / scale) wherever that provably
+//    gives the same code.  q' = fl(x * fl(1/s)) is within 1.5 ulp of the
+//    correctly rounded x / s, so both encode to the same code unless they
+//    can straddle an RNE decision point.  In the normal range those are the
+//    midpoints between codes, whose 20 dropped mantissa bits are exactly
+//    0x80000 (no midpoint lies near a binade edge); a q' within 8 ulp of one
+//    is recomputed with the IEEE division.  So are the subnormal range
+//    (|q'| < 2^-6, where the decision points sit elsewhere in the bits; a
+//    small share of real data, handled off the common path), NaNs, and
+//    every element when the scale is not a positive normal number with a
+//    normal reciprocal.
+// 2. The encode uses gfx950's v_cvt_pk_fp8_f32 (RNE, OCP e4m3), which
+//    matches the format-defined encoder (e4m3_from_f32 above) on all 2^32
+//    fp32 inputs except NaNs of positive sign, which it encodes as 0xFF
+//    instead of 0x7F -- those never reach it (step 1 sends them to
+//    e4m3_from_f32).  The library's exhaustive device tests pin both.
+struct Fp8Quant {
+  float s, r;
+  bool fast;
+  __device__ __forceinline__ explicit Fp8Quant(float scale) : s(scale), r(1.0f / scale) {
+    const uint32_t es = (f2u(scale) >> 23) & 0x1FFu;  // sign + exponent
+    const uint32_t er = (f2u(r) >> 23) & 0x1FFu;
+    fast = es != 0u && es < 0xFFu && er != 0u && er < 0xFFu;
+  }
+  // Whether q' = x * r may encode differently from x / s (see above).
+  static __device__ __forceinline__ bool needs_division(float q) {
+    const uint32_t mag = f2u(q) & 0x7FFFFFFFu;
+    return (mag - 0x3C800000u) > (0x7F800000u - 0x3C800000u) || ((mag & 0xFFFFFu) - 0x7FFF8u) < 16u;
+  }
+  __device__ __forceinline__ uint8_t operator()(float x) const {
+    const float q = x * r;
+    if (__builtin_expect(!fast || needs_division(q), 0)) return e4m3_from_f32(x / s);
+    return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q, q, 0, false) & 0xFF);
+  }
+  // 16 values -> 16 codes, element e in byte e % 4 of word e / 4.
+  __device__ __forceinline__ uint4 pack16(const float* f) const {
+    uint32_t w[4];
+    uint32_t redo = 0u;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float q[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        q[j] = f[4 * g + j] * r;
+        redo |= (uint32_t)needs_division(q[j]) << (4 * g + j);
+      }
+      int v = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+      v = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], v, true);
+      w[g] = (uint32_t)v;
+    }
+    if (!fast) redo = 0xFFFFu;
+    if (__builtin_expect(redo != 0u, 0)) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        if ((redo >> e) & 1u) {
+          const uint32_t c = e4m3_from_f32(f[e] / s);
+          const int sh = 8 * (e & 3);
+          w[e >> 2] = (w[e >> 2] & ~(0xFFu << sh)) | (c << sh);
+        }
+      }
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
 // OCP e4m3fn code -> fp32 (exact).
 __device__ __forceinline__ float f32_from_e4m3(uint32_t c) {
   const uint32_t sign = (c & 0x80u) << 24;

@@ -111,4 +111,7 @@ struct ProfileScope {
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Compute units of the current device (cached per device; 256 if unknown).
+int device_cu_count();
+
 }  // namespace cf

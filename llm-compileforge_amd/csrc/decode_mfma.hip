@@ -111,6 +111,9 @@ struct Plan {
   int psum[kPlanMaxB + 1];  // first stream tile (within a KV head) of the sequence's runs
 };
 
+// LDS bytes of the plan, rounded up so what follows it is 16-byte aligned.
+constexpr size_t kPlanLdsBytes = (sizeof(Plan) + 15) & ~(size_t)15;
+
 // Pass 1: lengths; j0 <- tiles shared with the previous sequence;
 // psum <- first member of the sequence's group.  A sequence sharing fewer
 // than kMinShareTiles tiles with its predecessor starts a group; groups are
@@ -432,7 +435,27 @@ __device__ __forceinline__ void flush_run(const DecodeParams& p, const Index& ix
   }
 }
 
-template <int QT, int KT, int D, bool PL>
+// The stream range a launched wave takes (its "stream wave").  The stream
+// is head-major, so the ranges w, w + Wtot/Hkv, ... cover the same sequence
+// positions of the Hkv heads, i.e. the same blocks.  Workgroups are dealt
+// to the 8 XCDs round-robin (workgroup g on XCD g % 8), each with its own
+// L2, so the permutation gives the Hkv heads of one range to waves of the
+// same XCD, consecutive in the workgroup order: the heads of a block are
+// then read at about the same time from one XCD (adjacent 4 KiB tiles in
+// the paired layout; the 128-byte head slices of each token row in the
+// token-major layout).  A bijection on [0, Wtot) when the workgroups split
+// evenly over the XCDs and Hkv divides each XCD's waves, the identity
+// otherwise; it changes which wave does what, never the result.
+__device__ __forceinline__ int stream_wave(int w, int Wtot, int Hkv) {
+  constexpr int kXcds = 8;
+  if (Hkv <= 1 || Wtot % (4 * kXcds) != 0 || (Wtot / kXcds) % Hkv != 0) return w;
+  const int g = w >> 2, i = w & 3;
+  const int x = g % kXcds, lw = (g / kXcds) * 4 + i;  // XCD, wave index within it
+  const int k = x * (Wtot / kXcds / Hkv) + lw / Hkv;     // range among the Wtot / Hkv per head
+  return (lw % Hkv) * (Wtot / Hkv) + k;
+}
+
+template <int QT, int KT, int D, bool PL, bool VTOK>
 __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, const int32_t* __restrict__ tables,
                                                             const int32_t* __restrict__ lens,
                                                             const float* __restrict__ kscale,
@@ -447,8 +470,8 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   const int lane = threadIdx.x & 63;
   const int li = lane & 15, lq = lane >> 4;
   const int wave = uniform(threadIdx.x >> 6);
-  const int w = uniform(blockIdx.x * 4 + wave);
   const int Wtot = gridDim.x * 4;
+  const int w = uniform(stream_wave(blockIdx.x * 4 + wave, Wtot, p.Hkv));
 
   if constexpr (PL) {
     if (wave == 0) plan_pass1(p, ix, shared, pl, lane);
@@ -512,9 +535,13 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   bool has1 = next_slot<PL>(c0) < v_end;
   if (has1) c1 = advance(p, ix, seqs, c0);
 
-  const KvCacheView kv{(const uint8_t*)p.k, (const uint8_t*)p.v, p.k_s[0], p.k_s[2], p.v_s[0], p.v_s[2]};
-  TileRegs<KT, D> r0, r1;
-  load_tile<KT, D>(r0, kv, c0.blkA, c0.blkB, li, lq, c0.h);
+  const KvCacheView kv{(const uint8_t*)p.k, (const uint8_t*)p.v, p.k_s[0], p.k_s[2], p.v_s[0], p.v_s[2],
+                       p.k_s[1], p.v_s[1]};
+  // token-major V: this wave's LDS staging rows, after the plan
+  uint8_t* vstage = (uint8_t*)dyn_lds + (PL ? kPlanLdsBytes : 0) + wave * vtok_stage_bytes<D>();
+  (void)vstage;
+  TileRegs<KT, D, VTOK> r0, r1;
+  load_tile<KT, D, VTOK>(r0, kv, c0.blkA, c0.blkB, li, lq, c0.h, lane);
 
   QOp<QT> qop[NC];
   load_q<QT, D>(qop, p, c0, li, lq);
@@ -535,7 +562,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     // Always issue the next tile's loads (the last iteration reloads its
     // own tile) so every path has the same number of loads in flight and
     // the compiler's vmcnt waits stay exact.
-    load_tile<KT, D>(r1, kv, c1.blkA, c1.blkB, li, lq, c1.h);
+    load_tile<KT, D, VTOK>(r1, kv, c1.blkA, c1.blkB, li, lq, c1.h, lane);
     const bool has2 = has1 && next_slot<PL>(c1) < v_end;
     Coord c2 = c1;
     if (has2) c2 = advance(p, ix, seqs, c1);
@@ -559,6 +586,26 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     // Tiles at a sequence's end or with an invalid block are the only ones
     // with masked tokens (a wave-uniform condition).
     const bool partial = c0.len - 32 * c0.j < 32 || c0.blkA < 0 || c0.blkB < 0;
+    // V operands of the P.V product: loaded channel-major, or (VTOK) staged
+    // in LDS and read back transposed
+    using VT = typename TileRegs<KT, D, VTOK>::VT;
+    VT vraw[NV];
+    if constexpr (VTOK) {
+      static_assert(KT == kE4M3, "token-major V: e4m3 caches only");
+      // the previous tile's transposed reads are done before its rows are overwritten
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      vtok_stage<D>(vstage, r0.v, lane);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int t = 0; t < NV; ++t) vraw[t] = vtok_operand<D>(vstage, t, li, lq);
+    } else {
+#pragma unroll
+      for (int t = 0; t < NV; ++t) vraw[t] = r0.v[t];
+    }
     int nvalid = 8;
     if (partial) {
       const bool blk_ok = (lq < 2 ? c0.blkA : c0.blkB) >= 0;
@@ -567,7 +614,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
       for (int v = 0; v < 8; ++v)
         if (v >= nvalid) sc[v] = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < NV; ++t) r0.v[t] = mask_tokens(r0.v[t], nvalid);
+      for (int t = 0; t < NV; ++t) vraw[t] = mask_tokens(vraw[t], nvalid);
     }
     float mt = sc[0];
 #pragma unroll
@@ -608,8 +655,8 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
 #pragma unroll
       for (int t = 0; t < NV; ++t) {
         f16x8_t vop;
-        if constexpr (KT == kE4M3) vop = e4m3x8_to_f16(r0.v[t].x, r0.v[t].y);
-        else vop = __builtin_bit_cast(f16x8_t, r0.v[t]);
+        if constexpr (KT == kE4M3) vop = e4m3x8_to_f16(vraw[t].x, vraw[t].y);
+        else vop = __builtin_bit_cast(f16x8_t, vraw[t]);
         o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, o[t], 0, 0, 0);
       }
     } else {
@@ -623,7 +670,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
       }
 #pragma unroll
       for (int t = 0; t < NV; ++t) {
-        const bf16x8_t vop = as_bf16x8(r0.v[t]);
+        const bf16x8_t vop = as_bf16x8(vraw[t]);
         o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, o[t], 0, 0, 0);
         o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo, o[t], 0, 0, 0);
       }
@@ -885,13 +932,18 @@ int cu_count() {
 // Llama-3-8B shape).  The workspace holds slots for this many waves.
 constexpr int kStreamBlocksPerCU = 1;
 
-template <int QT, int KT, int D, bool PL>
+template <int D, bool PL, bool VTOK>
+constexpr size_t stream_lds_bytes() {
+  return (PL ? kPlanLdsBytes : 0) + (VTOK ? 4 * (size_t)vtok_stage_bytes<D>() : 0);
+}
+
+template <int QT, int KT, int D, bool PL, bool VTOK>
 int blocks_per_cu() {
   static int cached = 0;
   if (cached == 0) {
     int n = 0;
-    const size_t lds = PL ? sizeof(Plan) : 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<QT, KT, D, PL>, 256, lds) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<QT, KT, D, PL, VTOK>, 256,
+                                                     stream_lds_bytes<D, PL, VTOK>()) != hipSuccess ||
         n < 1)
       n = 1;
     cached = n < kStreamBlocksPerCU ? n : kStreamBlocksPerCU;
@@ -899,20 +951,34 @@ int blocks_per_cu() {
   return cached;
 }
 
-template <int QT, int KT, int D, bool PL>
+template <int QT, int KT, int D, bool PL, bool VTOK>
 int32_t launch_stream_t(const DecodeParams& p, hipStream_t stream) {
-  const int blocks = cu_count() * blocks_per_cu<QT, KT, D, PL>();
+  const int blocks = cu_count() * blocks_per_cu<QT, KT, D, PL, VTOK>();
   ProfileScope prof("cf_decode_mfma", stream);
-  CF_LAUNCH((decode_stream_kernel<QT, KT, D, PL>), dim3(blocks), dim3(256), PL ? sizeof(Plan) : 0, stream, p,
-                     p.tables, p.seq_lens, p.k_scale, p.v_scale, PL ? p.shared : nullptr);
+  CF_LAUNCH((decode_stream_kernel<QT, KT, D, PL, VTOK>), dim3(blocks), dim3(256), (stream_lds_bytes<D, PL, VTOK>()),
+            stream, p, p.tables, p.seq_lens, p.k_scale, p.v_scale, PL ? p.shared : nullptr);
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
 }
 
+// Whether V is token-major (the reference's [NB, bs, Hkv, D] order, unit
+// channel stride) rather than the native channel-major tile.
+bool v_token_major(const DecodeParams& p) { return p.v_s[3] == 1 && p.v_s[1] != 1; }
+
+template <int QT, int KT, int D, bool VTOK>
+int32_t launch_pl(const DecodeParams& p, hipStream_t stream) {
+  return p.B <= kPlanMaxB ? launch_stream_t<QT, KT, D, true, VTOK>(p, stream)
+                          : launch_stream_t<QT, KT, D, false, VTOK>(p, stream);
+}
+
 template <int QT, int KT, int D>
 int32_t launch_t(const DecodeParams& p, hipStream_t stream) {
-  const int32_t rc = p.B <= kPlanMaxB ? launch_stream_t<QT, KT, D, true>(p, stream)
-                                      : launch_stream_t<QT, KT, D, false>(p, stream);
+  int32_t rc;
+  if constexpr (KT == kE4M3) {
+    rc = v_token_major(p) ? launch_pl<QT, KT, D, true>(p, stream) : launch_pl<QT, KT, D, false>(p, stream);
+  } else {
+    rc = launch_pl<QT, KT, D, false>(p, stream);
+  }
   if (rc) return rc;
   const dim3 grid(p.Hkv, p.B);
   ProfileScope prof("cf_decode_merge", stream);
@@ -977,12 +1043,20 @@ bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
   // partial-row indices and descriptors are int32
   if ((uint64_t)total_rows(p.B, p.Hq) >= (uint64_t)INT32_MAX / 2) return false;
   const int kb = kv_dt == kE4M3 ? 1 : 2;
-  // Native layout: K tile [bs][D] (token stride D, channel stride 1), V tile
-  // [D][bs] (token stride 1, channel stride bs); block/head strides free.
-  if (p.k_s[3] != 1 || p.k_s[1] != p.D || p.v_s[1] != 1 || p.v_s[3] != 16) return false;
+  // K: token rows with unit channel stride, 16-byte aligned (token stride D
+  // in the native / paired layouts, any multiple of 16 bytes token-major).
+  // V: the native tile [D][bs] (token stride 1, channel stride bs), or
+  // token-major rows (channel stride 1; e4m3 only) -- block/head strides free.
+  if (p.k_s[3] != 1) return false;
   for (int i = 0; i < 3; ++i)
     if ((p.k_s[i] * kb) % 16 != 0) return false;
-  if ((p.v_s[0] * kb) % 16 != 0 || (p.v_s[2] * kb) % 16 != 0 || (p.v_s[3] * kb) % 16 != 0) return false;
+  const bool v_native = p.v_s[1] == 1 && p.v_s[3] == 16;
+  const bool v_tok = kv_dt == kE4M3 && p.v_s[3] == 1 && p.v_s[1] != 1 && (p.v_s[1] * kb) % 16 == 0;
+  if (!v_native && !v_tok) return false;
+  // native V rides with the native K tile (token stride D)
+  if (v_native && p.k_s[1] != p.D) return false;
+  if ((p.v_s[0] * kb) % 16 != 0 || (p.v_s[2] * kb) % 16 != 0) return false;
+  if (v_native && (p.v_s[3] * kb) % 16 != 0) return false;
   if (!aligned16(p.k) || !aligned16(p.v)) return false;
   // q rows: 16-byte aligned slices; out rows: 8-byte aligned groups of 4.
   if (!aligned16(p.q) || (p.q_sb * 2) % 16 != 0 || (p.q_sh * 2) % 16 != 0) return false;

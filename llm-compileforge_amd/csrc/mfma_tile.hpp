@@ -66,37 +66,41 @@ struct KvTraits<kF16> {
   static constexpr int kBytes = 2;
 };
 
-// Raw per-lane registers of one 32-token tile.
-template <int KT, int D>
+// Raw per-lane registers of one 32-token tile.  VTOK: V stored token-major
+// (the reference's [NB, bs, Hkv, D] order): the tile's 32 V rows are loaded
+// as 16-byte row pieces and transposed through LDS before the P.V product.
+template <int KT, int D, bool VTOK = false>
 struct TileRegs {
   static constexpr int KB = KvTraits<KT>::kBytes;
   static constexpr int KCHUNK = D / 4 * KB / 16;  // uint4 per K row slice
   static constexpr int NV = D / 16;
   uint4 k1[KCHUNK];  // K row slice of token 8*(i/4) + i%4
   uint4 k2[KCHUNK];  // ... and of that token + 4
-  // V: 8 tokens of one channel per PV MFMA (8 bytes e4m3, 16 bytes bf16)
+  // channel-major V: 8 tokens of one channel per PV MFMA (8 bytes e4m3,
+  // 16 bytes bf16); token-major V: 16-byte pieces of the 32 x D tile
   using VT = typename std::conditional<KB == 1, uint2, uint4>::type;
-  VT v[NV];
+  static constexpr int NVR = VTOK ? 32 * D * KB / (64 * 16) : NV;
+  using VR = typename std::conditional<VTOK, uint4, VT>::type;
+  VR v[NVR];
 };
 
-// Loads one 32-token tile (blocks blkA, blkB of KV head h) in the native
-// layout: K tile [bs][D] (token rows), V tile [D][bs] (channel rows), each
-// (block, head) tile contiguous.  Inner offsets are compile-time constants
-// (immediate offsets of the loads); block/head strides are uniform.
+// Loads one 32-token tile (blocks blkA, blkB of KV head h).  K: token rows
+// of D elements with unit channel stride, token stride kv.k_tok (D in the
+// native / paired layouts, Hkv * D token-major).  V: the native tile
+// [D][bs] (channel rows) or, VTOK, token rows at stride kv.v_tok.
 // Invalid blocks (id -1) read block 0 instead; their tokens are masked.
-// A paged KV cache in the native layout: base pointers and the block and
-// head strides (elements) of the K and V views.
 struct KvCacheView {
   const uint8_t* k;
   const uint8_t* v;
   int64_t k_blk, k_head, v_blk, v_head;
+  int64_t k_tok, v_tok;  // token strides (elements)
 };
 
-template <int KT, int D>
-__device__ __forceinline__ void load_tile(TileRegs<KT, D>& r, const KvCacheView& kv, int blkA, int blkB, int li,
-                                          int lq, int h) {
+template <int KT, int D, bool VTOK = false>
+__device__ __forceinline__ void load_tile(TileRegs<KT, D, VTOK>& r, const KvCacheView& kv, int blkA, int blkB, int li,
+                                          int lq, int h, int lane) {
   constexpr int KB = KvTraits<KT>::kBytes;
-  using R = TileRegs<KT, D>;
+  using R = TileRegs<KT, D, VTOK>;
   const int64_t a = blkA < 0 ? 0 : blkA, bb = blkB < 0 ? 0 : blkB;
   const uint8_t* kA = kv.k + (a * kv.k_blk + (int64_t)h * kv.k_head) * KB;
   const uint8_t* kB = kv.k + (bb * kv.k_blk + (int64_t)h * kv.k_head) * KB;
@@ -105,17 +109,64 @@ __device__ __forceinline__ void load_tile(TileRegs<KT, D>& r, const KvCacheView&
   // K: lane (li, lq) reads token koff = 8*(li/4)%16 + li%4 (+4) of block A
   // (li < 8) or B, channels [lq*D/4, (lq+1)*D/4).
   const int koff = (8 * (li >> 2) + (li & 3)) & 15;
-  const uint8_t* k1 = (li < 8 ? kA : kB) + (koff * D + lq * (D / 4)) * KB;
+  const int64_t ktok = VTOK ? kv.k_tok : D;
+  const uint8_t* k1 = (li < 8 ? kA : kB) + (koff * ktok + lq * (D / 4)) * KB;
 #pragma unroll
   for (int c = 0; c < R::KCHUNK; ++c) {
     r.k1[c] = stream_load<uint4>(k1 + 16 * c);
-    r.k2[c] = stream_load<uint4>(k1 + 4 * D * KB + 16 * c);
+    r.k2[c] = stream_load<uint4>(k1 + 4 * ktok * KB + 16 * c);
   }
-  // V: lane (li, lq) reads channel 16t + li, tokens 8*(lq%2)..+7 of block A
-  // (lq < 2) or B.
-  const uint8_t* vp = (lq < 2 ? vA : vB) + (li * 16 + (lq & 1) * 8) * KB;
+  if constexpr (VTOK) {
+    // row piece i of lane l: token row l / LPR + RPI * i, bytes (l % LPR) * 16
+    constexpr int LPR = D * KB / 16, RPI = 64 / LPR;
 #pragma unroll
-  for (int t = 0; t < R::NV; ++t) r.v[t] = stream_load<typename R::VT>(vp + t * 256 * KB);
+    for (int i = 0; i < R::NVR; ++i) {
+      const int row = lane / LPR + RPI * i;
+      r.v[i] = stream_load<uint4>((row < 16 ? vA : vB) + ((row & 15) * kv.v_tok) * KB + (lane % LPR) * 16);
+    }
+  } else {
+    // V: lane (li, lq) reads channel 16t + li, tokens 8*(lq%2)..+7 of block A
+    // (lq < 2) or B.
+    const uint8_t* vp = (lq < 2 ? vA : vB) + (li * 16 + (lq & 1) * 8) * KB;
+#pragma unroll
+    for (int t = 0; t < R::NV; ++t) r.v[t] = stream_load<typename R::VT>(vp + t * 256 * KB);
+  }
+}
+
+// Token-major V, e4m3: the wave's LDS staging area holds the tile's 32 token
+// rows at kVtokRowStride bytes each (the row pieces exactly as loaded), and
+// ds_read_b64_tr_b8 returns the channel-major operand: within each group of
+// 16 lanes, lane L receives byte L % 8 of the 8-byte words supplied by lanes
+// 2j + L / 8 (j = 0..7).  Lane (li, lq) of PV step t therefore points lanes
+// 2j + b at token 8 lq + j, channels 16 t + 8 b .. + 7, and receives channel
+// 16 t + li of tokens 8 lq .. 8 lq + 7 -- the operand the native layout
+// loads straight from HBM.  The row stride's 16-byte pad keeps the 8 rows a
+// group reads in distinct banks.
+template <int D>
+constexpr int vtok_row_stride() {
+  return D + 16;
+}
+template <int D>
+constexpr int vtok_stage_bytes() {
+  return 32 * vtok_row_stride<D>();
+}
+
+template <int D>
+__device__ __forceinline__ void vtok_stage(uint8_t* stage, const uint4* v, int lane) {
+  constexpr int LPR = D / 16, RPI = 64 / LPR, NVR = 32 * D / (64 * 16);
+#pragma unroll
+  for (int i = 0; i < NVR; ++i)
+    *(uint4*)(stage + (lane / LPR + RPI * i) * vtok_row_stride<D>() + (lane % LPR) * 16) = v[i];
+}
+
+typedef int v2i32_t __attribute__((ext_vector_type(2)));
+
+template <int D>
+__device__ __forceinline__ uint2 vtok_operand(const uint8_t* stage, int t, int li, int lq) {
+  const uint8_t* src = stage + (8 * lq + (li >> 1)) * vtok_row_stride<D>() + 16 * t + 8 * (li & 1);
+  const v2i32_t r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+      (__attribute__((address_space(3))) v2i32_t*)((__attribute__((address_space(3))) const uint8_t*)src));
+  return make_uint2((uint32_t)r.x, (uint32_t)r.y);
 }
 
 // Keeps the first `nbytes` bytes of an 8-byte register pair, zeroing the rest.

@@ -455,3 +455,75 @@ def test_full_c4_llama3_70b(gpu):
     k2, v2, inv = _permuted_paired(kc, vc, gpu, seed=6)
     out2 = _run(case, k2, v2, ks, vs, gpu, tables=inv[tables.long()].to(torch.int32))
     assert torch.equal(out2, out)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 2, 128), (32, 2, 64)])
+def test_token_major_fp8_on_the_mfma_path(gpu, hq, hkv, d):
+    """e4m3 caches in the reference's own token-major layout ([NB, bs, Hkv, D])
+    run the MFMA kernel (V staged through LDS and read back transposed);
+    lengths ending mid-block and mid-tile, one token, an invalid block id and
+    a shared-prefix statement; outputs bitwise equal to the native layout's
+    (the same operands reach the same MFMAs) and to the oracle's bound."""
+    print(f"[case] token-major e4m3 hq={hq} hkv={hkv} d={d}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(hq + 7 * d)
+    lens = [1, 15, 33, 700, 1024 + 40, 1024 + 100, 2000]
+    nb = 400
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(5)).tolist()
+    shared = perm[:64]
+    tables, pos = [], 64
+    for i, n in enumerate(lens):
+        k = (n + 15) // 16
+        if i in (4, 5):
+            tables.append(shared + perm[pos:pos + k - 64])
+            pos += k - 64
+        else:
+            tables.append(perm[pos:pos + k])
+            pos += k
+    q = torch.randn(len(lens), hq, d, generator=g, device=gpu).to(torch.bfloat16)
+    ksrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
+    vsrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
+    case = workloads.DecodeCase("tok", q, ksrc, vsrc, tables, lens, 16, 1 / math.sqrt(d), torch.float8_e4m3fn)
+    kt, vt, ks, vs = workloads.materialize(case, "token_major")
+    assert L.layout_of(kt, False) == "token_major" and L.layout_of(vt, True) == "token_major"
+    kn, vn, _, _ = workloads.materialize(case, "native")
+    tab = case.tables_tensor(gpu)
+    bad = tab.clone()
+    bad[3, 7] = nb + 3  # an invalid block in the middle of sequence 3
+    sh = torch.tensor(ops.shared_prefix_lens(tables, lens, 16), dtype=torch.int32, device=gpu)
+    with ops.KernelTimer() as timer:
+        out_t = paged_attention_tensors(q, kt, vt, bad, case.seq_lens_tensor(gpu), 16, case.scale, k_scale=ks,
+                                        v_scale=vs, shared_prefix_lens=sh)
+        out_n = paged_attention_tensors(q, kn, vn, bad, case.seq_lens_tensor(gpu), 16, case.scale, k_scale=ks,
+                                        v_scale=vs, shared_prefix_lens=sh)
+        torch.cuda.synchronize()
+        assert timer.query("cf_decode_mfma")[1] == 2 and timer.query("cf_decode_generic")[1] == 0
+    assert torch.equal(out_t, out_n)
+    t3 = tables[3][:7] + tables[3][8:]
+    eff = list(lens)
+    eff[3] -= 16
+    ref = oracle_decode(case, kt, vt, ks, vs, tables=tables[:3] + [t3] + tables[4:], lens=eff)
+    assert_close(out_t.float().cpu().numpy(), ref, torch.bfloat16, f"token-major {hq}/{hkv}/{d}")
+
+
+def test_full_c3_token_major(gpu):
+    """The headline config in the reference's token-major layout at full size:
+    the MFMA path, bitwise equal to the paired layout's output, and the
+    oracle on 16 sampled sequences."""
+    print("[case] c3 full size, token-major layout", flush=True)
+    case = workloads.make_case("c3_llama3_8b", device=gpu, seed=0)
+    kt, vt, ks, vs = workloads.materialize(case, "token_major")
+    kp, vp, _, _ = workloads.materialize(case, "paired")
+    tables, lens = case.tables_tensor(gpu), case.seq_lens_tensor(gpu)
+    sh = torch.tensor(ops.shared_prefix_lens(case.block_tables, case.seq_lens, 16), dtype=torch.int32, device=gpu)
+    with ops.KernelTimer() as timer:
+        out_t = ops.DecodePlan(case.q, kt, vt, tables, lens, case.scale, 16, ks, vs, shared_prefix_lens=sh).run()
+        torch.cuda.synchronize()
+        assert timer.query("cf_decode_mfma")[1] == 1
+    out_p = ops.DecodePlan(case.q, kp, vp, tables, lens, case.scale, 16, ks, vs, shared_prefix_lens=sh).run()
+    torch.cuda.synchronize()
+    assert torch.equal(out_t, out_p)
+    idx = _sample_ids(case.seq_lens, [0, 1, 31, 32, 63], 9, seed=3)
+    sub = workloads.DecodeCase("c3_tok", case.q[idx], case.k, case.v, [case.block_tables[i] for i in idx],
+                               [case.seq_lens[i] for i in idx], 16, case.scale, case.kv_dtype)
+    ref = oracle_decode(sub, kt, vt, ks, vs)
+    assert_close(out_t[idx].float().cpu().numpy(), ref, torch.bfloat16, "c3 token-major")

@@ -36,6 +36,37 @@ def test_device_encoder_exhaustive(gpu):
     assert bad == 0
 
 
+def test_quantize_with_a_scale_exhaustive(gpu):
+    """All 2^32 float32 patterns divided by a scale that is not a power of
+    two (x * (1/s) and x / s then differ in the last bit for many inputs):
+    the device codes equal the oracle's IEEE division then RNE encode."""
+    s = 0.0671234
+    sc = torch.full((1,), s, dtype=torch.float32, device=gpu)
+    chunk = 1 << 28
+    bad = 0
+    for start in range(0, 1 << 32, chunk):
+        bits = torch.arange(start, start + chunk, dtype=torch.int64, device=gpu).to(torch.int32)
+        got = ops.fp8_quantize(bits.view(torch.float32).view(1, 1, -1), sc).view(torch.uint8).view(-1).cpu().numpy()
+        x = np.arange(start, start + chunk, dtype=np.uint32).view(np.float32)
+        bad += int(np.count_nonzero(got != ofp8.quantize(x, s)))
+        del bits, x
+    print(f"[fp8] exhaustive mismatches with scale {s}: {bad}", flush=True)
+    assert bad == 0
+
+
+@pytest.mark.parametrize("s", [3.0, 1.0 / 3.0, 1.234e-5, 7.77e3, 1e-12, 1e-39, 3e38])
+def test_quantize_scales_on_random_patterns(gpu, s):
+    """2^26 random float32 patterns (every exponent, NaN and inf included)
+    per scale, including scales whose reciprocal is not normal."""
+    g = torch.Generator(device=gpu).manual_seed(int(s * 1000) % 997)
+    bits = torch.randint(-(2**31), 2**31, (1 << 26,), generator=g, device=gpu, dtype=torch.int64).to(torch.int32)
+    x = bits.view(torch.float32)
+    sc = torch.full((1,), s, dtype=torch.float32, device=gpu)
+    got = ops.fp8_quantize(x.view(1, 1, -1), sc).view(torch.uint8).view(-1).cpu().numpy()
+    want = ofp8.quantize(x.cpu().numpy(), np.float32(s))
+    assert np.array_equal(got, want), int(np.count_nonzero(got != want))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_per_head_quantize_bit_exact(gpu, dtype):
     g = torch.Generator(device=gpu).manual_seed(1)
