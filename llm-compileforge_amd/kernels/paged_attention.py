@@ -27,11 +27,17 @@ import torch
 
 from cf_hip import ops as _ops
 
-# Pinned staging for the dict API's tables / lengths / shared-prefix
-# statement: two buffers per device, each reused once the copy that last
-# read it has run (an event per buffer), so a call allocates no pinned
-# memory and never waits on the GPU in steady state.
-_STAGE: dict[torch.device, list] = {}
+# Staging for the dict API's tables / lengths / shared-prefix statement:
+# per (device, stream), _SLOTS slots of {pinned host buffer, device buffer}.
+# A call packs into a slot's host buffer, copies it into the slot's device
+# buffer on the stream and records an event; the slot is reused _SLOTS
+# calls later, after that event (the host buffer is free once its copy ran;
+# the device buffer is read by this stream's earlier kernels only, which
+# precede the new copy).  No call allocates in steady state, and calls
+# issued back to back wait on the GPU only when the host runs _SLOTS calls
+# ahead of it.
+_SLOTS = 4
+_STAGE: dict[tuple[torch.device, int], list] = {}
 
 
 def _pack_tables_py(block_tables: dict, seq_lens: dict, block_size: int, nb: int, out: np.ndarray,
@@ -109,22 +115,29 @@ def _as_ids(blocks) -> np.ndarray:
     return np.asarray(blocks, dtype=np.int64)
 
 
-def _staging(device: torch.device, n: int) -> torch.Tensor:
-    st = _STAGE.setdefault(device, [[None, None], [None, None], 0])
-    bufs, events, k = st
+def _staging(device: torch.device, n: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(pinned host buffer, device buffer) of the next slot, each >= n int32."""
+    key = (device, _ops.stream_handle(device))
+    st = _STAGE.get(key)
+    if st is None:
+        st = _STAGE[key] = [[None] * _SLOTS, [None] * _SLOTS, [None] * _SLOTS, 0]
+    hosts, devs, events, k = st
     if events[k] is not None:
         events[k].synchronize()
-    if bufs[k] is None or bufs[k].numel() < n:
-        bufs[k] = torch.empty(max(n, 1 << 16), dtype=torch.int32, pin_memory=True)
-    return bufs[k]
+    if hosts[k] is None or hosts[k].numel() < n:
+        size = max(n, 1 << 16)
+        hosts[k] = torch.empty(size, dtype=torch.int32, pin_memory=True)
+        devs[k] = torch.empty(size, dtype=torch.int32, device=device)
+    return hosts[k], devs[k]
 
 
 def _staged(device: torch.device) -> None:
-    st = _STAGE[device]
-    ev = torch.cuda.Event()
+    st = _STAGE[(device, _ops.stream_handle(device))]
+    ev = st[2][st[3]]
+    if ev is None:
+        ev = st[2][st[3]] = torch.cuda.Event()
     ev.record(torch.cuda.current_stream(device))
-    st[1][st[2]] = ev
-    st[2] ^= 1
+    st[3] = (st[3] + 1) % _SLOTS
 
 DEFAULT_PARTITION_TOKENS = _ops.DEFAULT_PARTITION_TOKENS
 
@@ -230,9 +243,11 @@ def paged_attention(
     nb = k_cache.shape[0]
     n_req = len(rids)
     width = table_width(block_tables)
-    host = _staging(q.device, n_req * (width + 2))
+    host, dbuf = _staging(q.device, n_req * (width + 2))
     mb = pack_tables(block_tables, seq_lens, block_size, nb, host.numpy(), width)
-    dev = host[: n_req * (mb + 2)].to(q.device, non_blocking=True)
+    used = n_req * (mb + 2)
+    dev = dbuf[:used]
+    dev.copy_(host[:used], non_blocking=True)
     _staged(q.device)
     dev_tables = dev[: n_req * mb].view(n_req, mb)
     dev_lens = dev[n_req * mb: n_req * (mb + 1)]
