@@ -298,6 +298,16 @@ int32_t cf_paged_write(const CfTensor* x_new, const CfTensor* slot_mapping,
 int32_t cf_paged_gather(const CfTensor* cache, const CfTensor* block_tables,
                         const CfTensor* scale, CfTensor* out, void* stream);
 
+/* Uploads `bytes` (a multiple of 16; both pointers 16-byte aligned) from
+ * pinned, mapped host memory (hipHostMalloc, torch pin_memory) to device
+ * memory with a kernel on `stream`, so the upload is ordered with the
+ * stream's kernels on the compute queue (no copy-engine hand-off between
+ * back-to-back calls).  Fails with CF_ERR_INVALID if host_src is not mapped
+ * pinned memory or dev_dst is not device memory.  No reference counterpart:
+ * the upload of the tables the dict-based paged_attention packs on the host
+ * (reference kernels/paged_attention.py:200-227 takes host dicts). */
+int32_t cf_stage_from_host(const void* host_src, void* dev_dst, uint64_t bytes, void* stream);
+
 /* ---- Paged block pool (host) ---------------------------------------------
  * Replaces the reference's BlockManager (runtime/src/cache/block.rs:78-352;
  * Python binding PyBlockManager, runtime/src/lib.rs:82-168): reference-

@@ -195,6 +195,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "cf_bp_shared_prefix_lens": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
     "cf_block_tables_apply": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
     "cf_copy_blocks": (ctypes.c_int32, [_P, _P, ctypes.c_void_p]),
+    "cf_stage_from_host": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]),
     "cf_profile_enable": (ctypes.c_int32, [ctypes.c_int32]),
     "cf_profile_reset": (ctypes.c_int32, []),
     "cf_profile_query": (

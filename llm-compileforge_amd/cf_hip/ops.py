@@ -446,6 +446,19 @@ def paged_gather(
     return out
 
 
+def stage_from_host(host_ptr: int, dev_ptr: int, nbytes: int, device: torch.device) -> bool:
+    """Uploads nbytes (a multiple of 16) from mapped pinned host memory to
+    device memory with the library's upload kernel on the current stream;
+    False (nothing enqueued) when the host buffer is not mapped pinned
+    memory."""
+    with _on(device):
+        rc = lib().cf_stage_from_host(host_ptr, dev_ptr, nbytes, stream_handle(device))
+    if rc == _abi.CF_ERR_INVALID:
+        return False
+    check(rc, "cf_stage_from_host")
+    return True
+
+
 def block_tables_apply(table: torch.Tensor, lens: torch.Tensor, deltas: torch.Tensor) -> None:
     """Scatters block-table deltas [n, 4] int32 = {row, col, value, 0} into a
     device table [rows, cols] int32 (col = -1: lens[row] = value)."""
@@ -578,5 +591,6 @@ __all__ = [
     "paged_gather",
     "paged_write",
     "shared_prefix_lens",
+    "stage_from_host",
     "_abi",
 ]

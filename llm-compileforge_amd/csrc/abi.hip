@@ -750,6 +750,33 @@ int32_t cf_paged_gather(const CfTensor* cache, const CfTensor* block_tables, con
   return launch_paged_gather(p, vc.dtype, vo.dtype, as_stream(stream));
 }
 
+int32_t cf_stage_from_host(const void* host_src, void* dev_dst, uint64_t bytes, void* stream) {
+  CF_CHECK(host_src != nullptr && dev_dst != nullptr, "NULL pointer");
+  CF_CHECK(bytes % 16 == 0, "bytes (%llu) must be a multiple of 16", (unsigned long long)bytes);
+  CF_CHECK(((uintptr_t)host_src & 15) == 0 && ((uintptr_t)dev_dst & 15) == 0, "pointers must be 16-byte aligned");
+  if (bytes == 0) return CF_OK;
+  // The device's view of the host buffer; fails unless the memory is pinned
+  // and mapped (hipHostMalloc), so nothing else is ever dereferenced.
+  // A refused query also sets HIP's per-thread last error, which the caller's
+  // next runtime check (torch's, after its next launch) would report as its
+  // own failure: read it back here so the refusal stays this call's.
+  void* view = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&view, const_cast<void*>(host_src), 0);
+  if (e != hipSuccess || view == nullptr) {
+    (void)hipGetLastError();
+    set_error("host_src is not mapped pinned host memory (hipHostGetDevicePointer: %s)", hipGetErrorString(e));
+    return CF_ERR_INVALID;
+  }
+  hipPointerAttribute_t attr;
+  const hipError_t ea = hipPointerGetAttributes(&attr, dev_dst);
+  if (ea != hipSuccess || attr.type != hipMemoryTypeDevice) {
+    (void)hipGetLastError();
+    set_error("dev_dst is not device memory (hipPointerGetAttributes: %s)", hipGetErrorString(ea));
+    return CF_ERR_INVALID;
+  }
+  return launch_stage_from_host(view, dev_dst, bytes, as_stream(stream));
+}
+
 int32_t cf_profile_enable(int32_t on) {
   std::lock_guard<std::mutex> lock(g_prof_mu);
   g_prof_on = on != 0;

@@ -227,4 +227,25 @@ int32_t launch_paged_gather(const PagedGatherParams& p, int cache_dt, int out_dt
   return CF_OK;
 }
 
+// ---- upload of host-packed tables --------------------------------------------
+// Copies n 16-byte words from device-visible pinned host memory into device
+// memory: the upload rides the compute queue with the kernels that read it,
+// so back-to-back calls hand nothing between the copy engine and the
+// compute queue.  Host memory is read once: plain vector loads.
+__global__ __launch_bounds__(256) void stage_from_host_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                              int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) dst[i] = src[i];
+}
+
+int32_t launch_stage_from_host(const void* src_dev_view, void* dst, uint64_t bytes, hipStream_t stream) {
+  const int64_t n = (int64_t)(bytes / 16);
+  if (n == 0) return CF_OK;
+  const int64_t blocks = std::min<int64_t>(ceil_div(n, 256), 64);
+  ProfileScope prof("cf_stage_from_host", stream);
+  CF_LAUNCH(stage_from_host_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint4*)src_dev_view,
+            (uint4*)dst, n);
+  CF_HIP_CHECK(hipGetLastError());
+  return CF_OK;
+}
+
 }  // namespace cf

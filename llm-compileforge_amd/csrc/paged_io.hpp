@@ -36,5 +36,7 @@ struct PagedGatherParams {
 
 int32_t launch_paged_write(const PagedWriteParams& p, int x_dt, int slot_dt, int cache_dt, hipStream_t stream);
 int32_t launch_paged_gather(const PagedGatherParams& p, int cache_dt, int out_dt, hipStream_t stream);
+// bytes (a multiple of 16) from a device-visible view of pinned host memory.
+int32_t launch_stage_from_host(const void* src_dev_view, void* dst, uint64_t bytes, hipStream_t stream);
 
 }  // namespace cf

@@ -124,8 +124,8 @@ def _staging(device: torch.device, n: int) -> tuple[torch.Tensor, torch.Tensor]:
     hosts, devs, events, k = st
     if events[k] is not None:
         events[k].synchronize()
-    if hosts[k] is None or hosts[k].numel() < n:
-        size = max(n, 1 << 16)
+    if hosts[k] is None or hosts[k].numel() < n + 4:
+        size = max(n + 4, 1 << 16)  # + 4: the upload moves whole 16-byte words
         hosts[k] = torch.empty(size, dtype=torch.int32, pin_memory=True)
         devs[k] = torch.empty(size, dtype=torch.int32, device=device)
     return hosts[k], devs[k]
@@ -138,6 +138,17 @@ def _staged(device: torch.device) -> None:
         ev = st[2][st[3]] = torch.cuda.Event()
     ev.record(torch.cuda.current_stream(device))
     st[3] = (st[3] + 1) % _SLOTS
+
+def _upload(host: torch.Tensor, dbuf: torch.Tensor, n: int, device: torch.device) -> None:
+    """host[:n] -> dbuf[:n] on the current stream: with the library's
+    compute-queue upload (a kernel reading the pinned buffer, ordered with
+    the decode kernels without a copy-engine hand-off), or a torch copy where
+    the buffer is not mapped pinned memory."""
+    nbytes = ((n + 3) // 4) * 16
+    if _ops.stage_from_host(host.data_ptr(), dbuf.data_ptr(), nbytes, device):
+        return
+    dbuf[:n].copy_(host[:n], non_blocking=True)
+
 
 DEFAULT_PARTITION_TOKENS = _ops.DEFAULT_PARTITION_TOKENS
 
@@ -247,7 +258,7 @@ def paged_attention(
     mb = pack_tables(block_tables, seq_lens, block_size, nb, host.numpy(), width)
     used = n_req * (mb + 2)
     dev = dbuf[:used]
-    dev.copy_(host[:used], non_blocking=True)
+    _upload(host, dbuf, used, q.device)
     _staged(q.device)
     dev_tables = dev[: n_req * mb].view(n_req, mb)
     dev_lens = dev[n_req * mb: n_req * (mb + 1)]
