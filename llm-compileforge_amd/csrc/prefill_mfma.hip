@@ -186,7 +186,7 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
 #pragma unroll
   for (int i = 0; i < Gm::KPT; ++i) {
     const int u = tid + 256 * i;
-    if (u < Gm::KU) {
+    if (Gm::KU % 256 == 0 || u < Gm::KU) {
       const int s = u / (64 * Gm::KUPL), rem = u % (64 * Gm::KUPL);
       const int lane = rem % 64, cp = rem / 64;
       const int li = lane & 15, lq = lane >> 4;
@@ -200,7 +200,7 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
 #pragma unroll
   for (int i = 0; i < Gm::VPT; ++i) {
     const int u = tid + 256 * i;
-    if (u < Gm::VU) {
+    if (Gm::VU % 256 == 0 || u < Gm::VU) {
       // 16 bytes of channel d of block X: all 16 tokens (e4m3) or half of them (bf16)
       const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
       const int d = rem / Gm::VPER, part = rem % Gm::VPER;
@@ -216,14 +216,15 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
 // chain s; V entry (step t, lane) = channel 16 t + li, tokens 8 lq .. 8 lq + 7.
 // V tokens at or past `valid` (tile-relative) or in an invalid block become
 // zero (cache slots there may hold any bits, NaN codes included).
-template <int KT, int D>
+// FULL: the caller knows every token of the tile is valid.
+template <int KT, int D, bool FULL = false>
 __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const uint4* vr, const TileIds& t,
                                             int valid, int tid) {
   using Gm = Geo<KT, D>;
 #pragma unroll
   for (int i = 0; i < Gm::KPT; ++i) {
     const int u = tid + 256 * i;
-    if (u < Gm::KU) {
+    if (Gm::KU % 256 == 0 || u < Gm::KU) {
       const int s = u / (64 * Gm::KUPL), rem = u % (64 * Gm::KUPL);
       const int lane = rem % 64, cp = rem / 64;
       if constexpr (KT == kE4M3) {
@@ -237,11 +238,11 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
   uint4* vl = lds + Gm::KENT;
   // Tiles whose 32 tokens are all valid (all but an item's last tile) skip
   // the masking (a wave-uniform branch).
-  const bool full = valid >= 32 && t.va && t.vb;
+  const bool full = FULL || (valid >= 32 && t.va && t.vb);
 #pragma unroll
   for (int i = 0; i < Gm::VPT; ++i) {
     const int u = tid + 256 * i;
-    if (u < Gm::VU) {
+    if (Gm::VU % 256 == 0 || u < Gm::VU) {
       const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
       const int d = rem / Gm::VPER, part = rem % Gm::VPER;
       const bool ok = X ? t.vb : t.va;
@@ -262,6 +263,31 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
       } else {
         const int n0 = ok ? valid - 16 * X - 8 * part : 0;
         vl[tt * 64 + 32 * X + 16 * part + li] = mask_tokens(vr[i], n0);
+      }
+    }
+  }
+}
+
+// Zeroes, in the staged registers, the V tokens at or past `valid`
+// (tile-relative) or in an invalid block, so that the tile can then be
+// written without masking.
+template <int KT, int D>
+__device__ __forceinline__ void mask_staged_v(uint4* vr, const TileIds& t, int valid, int tid) {
+  using Gm = Geo<KT, D>;
+#pragma unroll
+  for (int i = 0; i < Gm::VPT; ++i) {
+    const int u = tid + 256 * i;
+    if (Gm::VU % 256 == 0 || u < Gm::VU) {
+      const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
+      const int part = rem % Gm::VPER;
+      const bool ok = X ? t.vb : t.va;
+      if constexpr (KT == kE4M3) {
+        const int n0 = ok ? valid - 16 * X : 0;
+        const uint2 lo = keep_bytes(make_uint2(vr[i].x, vr[i].y), n0);
+        const uint2 hi = keep_bytes(make_uint2(vr[i].z, vr[i].w), n0 - 8);
+        vr[i] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      } else {
+        vr[i] = mask_tokens(vr[i], ok ? valid - 16 * X - 8 * part : 0);
       }
     }
   }
@@ -313,15 +339,11 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
 #pragma unroll
       for (int c = 0; c < NC; ++c) qop[k][c] = as_bf16x8(*(const uint4*)(qrow + 8 * c));
     }
-    // tokens every column / some column of this wave may see
-    int lmin = min(lim[0], lim[1]), lmax = max(lim[0], lim[1]);
+    // tokens every column of this wave may see
+    int lmin = min(lim[0], lim[1]);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      lmin = min(lmin, __shfl_xor(lmin, o, 64));
-      lmax = max(lmax, __shfl_xor(lmax, o, 64));
-    }
+    for (int o = 32; o > 0; o >>= 1) lmin = min(lmin, __shfl_xor(lmin, o, 64));
     lmin = uniform(lmin);
-    lmax = uniform(lmax);
     float qk_scale = p.scale * (kscale ? kscale[h * p.ks_s] : 1.0f) * kLog2e;
     if (qk_scale < 0.0f) {
       // the softmax takes its max on raw scores: keep the scale positive by
@@ -355,122 +377,194 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
 #pragma unroll
       for (int t = 0; t < NV; ++t) o[k][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // K/V registers of two tiles in flight (kr[P], vr[P]) and the block ids
-    // of tiles j .. j + 3: tile j + 2 loads while tile j is computed and
-    // tile j + 1 goes from registers to LDS.
-    uint4 kr[2][Gm::KPT], vr[2][Gm::VPT];
+    // K/V registers of the tile in flight and the block ids of tiles j ..
+    // j + 3.  At the start of step j, tile j + 1 goes from the registers to
+    // the free LDS buffer and tile j + 2 starts loading into the same
+    // registers, while tile j is computed from the other buffer.  Past the
+    // item's last tile the ids repeat the last valid ones: the extra load
+    // reads real blocks and is never used.
+    uint4 kr[Gm::KPT], vr[Gm::VPT];
     TileIds id0 = tile_ids(p, tables, n, 0, kvlen);
     TileIds id1 = nt > 1 ? tile_ids(p, tables, n, 1, kvlen) : id0;
     TileIds id2 = nt > 2 ? tile_ids(p, tables, n, 2, kvlen) : id1;
-    if (nt > 0) stage_load<KT, D>(kr[0], vr[0], p, id0, h, tid);
-    if (nt > 1) stage_load<KT, D>(kr[1], vr[1], p, id1, h, tid);
-    if (nt > 0) stage_write<KT, D>(lds[0], kr[0], vr[0], id0, kvlen, tid);
+    if (nt > 0) {
+      stage_load<KT, D>(kr, vr, p, id0, h, tid);
+      stage_write<KT, D>(lds[0], kr, vr, id0, kvlen, tid);
+    }
+    if (nt > 1) stage_load<KT, D>(kr, vr, p, id1, h, tid);
     __syncthreads();
 
-    auto step = [&](auto par, int j) {
-      constexpr int P = decltype(par)::value;
-      if (j + 2 < nt) stage_load<KT, D>(kr[P], vr[P], p, id2, h, tid);
-      const TileIds id3 = j + 3 < nt ? tile_ids(p, tables, n, j + 3, kvlen) : id2;
-      if (32 * j < lmax) {
-        const uint4* kl = lds[P];
-        const uint4* vl = kl + Gm::KENT;
-        bf16x8_t a1[NC], a2[NC];
-        uint4 vraw[NV];
+    using POp = typename std::conditional<KT == kE4M3, f16x8_t, bf16x8_t>::type;
+
+    // The tile's math per column tile k, in pieces the step below orders so
+    // that each batch of MFMAs has independent VALU work beside it.
+    // Scores: lane (li, lq) holds s1[v] -> token tok0 + v, s2[v] -> token
+    // tok0 + 4 + v.
+    auto qk = [&](auto kc, const bf16x8_t* a1, const bf16x8_t* a2, f32x4_t& s1, f32x4_t& s2) {
+      constexpr int k = decltype(kc)::value;
+      s1 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      s2 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          a1[c] = as_bf16x8(kl[c * 64 + lane]);
-          a2[c] = as_bf16x8(kl[(NC + c) * 64 + lane]);
-        }
+      for (int c = 0; c < NC; ++c) {
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[c], qop[k][c], s1, 0, 0, 0);
+        s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[c], qop[k][c], s2, 0, 0, 0);
+      }
+    };
+    // Scores column tile k may not see (edge tiles only) become -inf, in
+    // place.
+    auto mask = [&](auto kc, f32x4_t& s1, f32x4_t& s2, bool blk_ok, int tok0) {
+      constexpr int k = decltype(kc)::value;
+      const int nvalid = blk_ok ? lim[k] - tok0 : 0;
 #pragma unroll
-        for (int t = 0; t < NV; ++t) vraw[t] = vl[t * 64 + lane];
-        const bool edge = 32 * j + 32 > lmin || !id0.va || !id0.vb;
-        const bool blk_ok = lq < 2 ? id0.va : id0.vb;
-        const int tok0 = 32 * j + 8 * lq;
-        using POp = typename std::conditional<KT == kE4M3, f16x8_t, bf16x8_t>::type;
-        POp pop[2], plo[2];
+      for (int v = 0; v < 4; ++v) {
+        if (v >= nvalid) s1[v] = -INFINITY;
+        if (v + 4 >= nvalid) s2[v] = -INFINITY;
+      }
+    };
+    // The lane's max of column tile k's scaled scores (qk_scale > 0: the
+    // max of the scaled scores, in log2 units).
+    auto lane_max = [&](const f32x4_t& s1, const f32x4_t& s2) {
+      float mt = fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]));
+      mt = fmaxf(mt, fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3])));
+      return mt * qk_scale;
+    };
+    // The lazy rescale of column tile k: the running max moves only when a
+    // score passes it by more than 8, so p <= 256.  The caller's lane-local
+    // test decides; the column max (across the 4 lanes of a column) is taken
+    // only then.
+    auto rescale = [&](auto kc, float mt) {
+      constexpr int k = decltype(kc)::value;
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float mnew = mt > m[k] + 8.0f ? mt : m[k];
+      const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[k] - mnew);
+      ol[k] = ol[k] * alpha;
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          f32x4_t s1 = {0.0f, 0.0f, 0.0f, 0.0f}, s2 = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int t = 0; t < NV; ++t) o[k][t] = o[k][t] * alpha;
+      m[k] = mnew;
+    };
+    // A column with nothing visible yet keeps m = -inf; its scores are all
+    // -inf, so any finite reference gives p = 0.
+    auto mref_of = [&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      return m[k] == -INFINITY ? 0.0f : m[k];
+    };
+    auto probs = [&](const f32x4_t& s1, const f32x4_t& s2, float mref, POp& pk, POp& pl) {
 #pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[c], qop[k][c], s1, 0, 0, 0);
-            s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[c], qop[k][c], s2, 0, 0, 0);
-          }
-          // lane (li, lq): s1[v] -> token tok0 + v, s2[v] -> token tok0 + 4 + v
-          float sc[8];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            sc[v] = s1[v];
-            sc[4 + v] = s2[v];
-          }
-          if (edge) {
-            const int nvalid = blk_ok ? lim[k] - tok0 : 0;
-#pragma unroll
-            for (int v = 0; v < 8; ++v)
-              if (v >= nvalid) sc[v] = -INFINITY;
-          }
-          float mt = sc[0];
-#pragma unroll
-          for (int v = 1; v < 8; ++v) mt = fmaxf(mt, sc[v]);
-          mt *= qk_scale;  // qk_scale > 0: the max of scaled scores (log2 units)
-          // lazy rescale: the running max moves only when a score passes it
-          // by more than 8, so p <= 256.  The lane-local test decides; the
-          // column max (across the 4 lanes of a column) is taken only then.
-          if (__any(mt > m[k] + 8.0f)) {
-            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-            const float mnew = mt > m[k] + 8.0f ? mt : m[k];
-            const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[k] - mnew);
-            ol[k] = ol[k] * alpha;
-#pragma unroll
-            for (int t = 0; t < NV; ++t) o[k][t] = o[k][t] * alpha;
-            m[k] = mnew;
-          }
-          // a column with nothing visible yet keeps m = -inf; its scores are
-          // all -inf, so any finite reference gives p = 0
-          const float mref = m[k] == -INFINITY ? 0.0f : m[k];
-#pragma unroll
-          for (int v = 0; v < 8; ++v) {
-            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], qk_scale, -mref));
-            if constexpr (KT == kE4M3) {
-              pop[k][v] = (_Float16)pv;
-            } else {
-              const __bf16 hi = (__bf16)pv;
-              pop[k][v] = hi;
-              plo[k][v] = (__bf16)(pv - (float)hi);
-            }
-          }
-        }
-        // ---- O^T += V^T P^T ------------------------------------------------
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          if constexpr (KT == kE4M3) {
-            const _Float16 one = li == 0 ? (_Float16)1.0f : (_Float16)0.0f;
-            const f16x8_t ones = {one, one, one, one, one, one, one, one};
-            ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[k], ol[k], 0, 0, 0);
-          } else {
-            const __bf16 one = li == 0 ? (__bf16)1.0f : (__bf16)0.0f;
-            const bf16x8_t ones = {one, one, one, one, one, one, one, one};
-            ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[k], ol[k], 0, 0, 0);
-            ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, plo[k], ol[k], 0, 0, 0);
-          }
-        }
-#pragma unroll
-        for (int t = 0; t < NV; ++t) {
-#pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            if constexpr (KT == kE4M3) {
-              o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, vraw[t]), pop[k], o[k][t],
-                                                               0, 0, 0);
-            } else {
-              const bf16x8_t vop = as_bf16x8(vraw[t]);
-              o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[k], o[k][t], 0, 0, 0);
-              o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo[k], o[k][t], 0, 0, 0);
-            }
-          }
+      for (int v = 0; v < 8; ++v) {
+        const float sv = v < 4 ? s1[v] : s2[v - 4];
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sv, qk_scale, -mref));
+        if constexpr (KT == kE4M3) {
+          pk[v] = (_Float16)pv;
+        } else {
+          const __bf16 hi = (__bf16)pv;
+          pk[v] = hi;
+          pl[v] = (__bf16)(pv - (float)hi);
         }
       }
-      if (j + 1 < nt) stage_write<KT, D>(lds[1 - P], kr[1 - P], vr[1 - P], id1, kvlen - 32 * (j + 1), tid);
+    };
+    // O^T += V^T P^T for column tile k; the row sums come out of the same
+    // pipe as O[column][0] against a V tile whose channel 0 is all ones.
+    auto pv = [&](auto kc, const uint4* vraw, const POp& pk, const POp& pl) {
+      constexpr int k = decltype(kc)::value;
+      if constexpr (KT == kE4M3) {
+        const _Float16 one = li == 0 ? (_Float16)1.0f : (_Float16)0.0f;
+        const f16x8_t ones = {one, one, one, one, one, one, one, one};
+        ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pk, ol[k], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < NV; ++t)
+          o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, vraw[t]), pk, o[k][t], 0, 0, 0);
+      } else {
+        const __bf16 one = li == 0 ? (__bf16)1.0f : (__bf16)0.0f;
+        const bf16x8_t ones = {one, one, one, one, one, one, one, one};
+        ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pk, ol[k], 0, 0, 0);
+        ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pl, ol[k], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+          const bf16x8_t vop = as_bf16x8(vraw[t]);
+          o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pk, o[k][t], 0, 0, 0);
+          o[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pl, o[k][t], 0, 0, 0);
+        }
+      }
+    };
+    // MFMAs of one column tile's P.V (or QK^T) product per batch below.
+    constexpr int kPvMfma = KT == kE4M3 ? NV + 1 : 2 * NV + 2;
+    constexpr int kQkMfma = 2 * NC;
+
+    // One step: the next tile's registers go to the other LDS buffer and
+    // the tile after it starts loading into them (interleaved with the
+    // first QK^T products), then tile j's math from buffer P.  The
+    // registers hold a whole valid tile here (mask_staged_v has zeroed what
+    // may not be read); on an item's last step they go to a buffer no one
+    // reads.  A wave whose columns see nothing of tile j still runs its
+    // math: every score is masked, so it adds exact zeros.
+    auto step = [&](auto par, int j) {
+      constexpr int P = decltype(par)::value;
+      const int valid_next = kvlen - 32 * (j + 1);
+      if (!(valid_next >= 32 && id1.va && id1.vb)) mask_staged_v<KT, D>(vr, id1, valid_next, tid);
+      const TileIds id3 = j + 3 < nt ? tile_ids(p, tables, n, j + 3, kvlen) : id2;
+      const uint4* kl = lds[P];
+      const uint4* vl = kl + Gm::KENT;
+      bf16x8_t a1[NC], a2[NC];
+      uint4 vraw[NV];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        a1[c] = as_bf16x8(kl[c * 64 + lane]);
+        a2[c] = as_bf16x8(kl[(NC + c) * 64 + lane]);
+      }
+      const bool edge = 32 * j + 32 > lmin || !id0.va || !id0.vb;
+      const bool blk_ok = lq < 2 ? id0.va : id0.vb;
+      const int tok0 = 32 * j + 8 * lq;
+      constexpr auto K0 = std::integral_constant<int, 0>{};
+      constexpr auto K1 = std::integral_constant<int, 1>{};
+      f32x4_t s1a, s2a, s1b, s2b;
+      POp pa, pla, pb, plb;
+      // QK^T of column tile 0 beside the next tile's conversion into LDS
+      qk(K0, a1, a2, s1a, s2a);
+      stage_write<KT, D, true>(lds[1 - P], kr, vr, id1, valid_next, tid);
+      stage_load<KT, D>(kr, vr, p, id2, h, tid);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * NC, 0);
+#pragma unroll
+      for (int i = 0; i < kQkMfma; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x020, Gm::KPT + Gm::VPT, 0);
+      if (edge) mask(K0, s1a, s2a, blk_ok, tok0);
+      // QK^T of column tile 1 beside column tile 0's max; the V operands
+      // are read from LDS meanwhile (not earlier: fewer registers live
+      // across the QK^T products)
+      qk(K1, a1, a2, s1b, s2b);
+      const float mta = lane_max(s1a, s2a);
+#pragma unroll
+      for (int t = 0; t < NV; ++t) vraw[t] = vl[t * 64 + lane];
+#pragma unroll
+      for (int i = 0; i < kQkMfma; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, NV / kQkMfma > 0 ? NV / kQkMfma : 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);
+      }
+      if (edge) mask(K1, s1b, s2b, blk_ok, tok0);
+      const float mtb = lane_max(s1b, s2b);
+      const bool up_a = mta > m[0] + 8.0f, up_b = mtb > m[1] + 8.0f;
+      if (__any(up_a || up_b)) {
+        rescale(K0, mta);
+        rescale(K1, mtb);
+      }
+      // exponentials of column tile 0, then its P.V beside the exponentials
+      // of column tile 1, then column tile 1's P.V
+      probs(s1a, s2a, mref_of(K0), pa, pla);
+      pv(K0, vraw, pa, pla);
+      probs(s1b, s2b, mref_of(K1), pb, plb);
+      pv(K1, vraw, pb, plb);
+      __builtin_amdgcn_sched_group_barrier(0x002, 20, 2);
+#pragma unroll
+      for (int i = 0; i < kPvMfma; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 2);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kPvMfma, 2);
       __syncthreads();
       id0 = id1;
       id1 = id2;

@@ -85,6 +85,27 @@ def test_per_head_quantize_bit_exact(gpu, dtype):
     assert scales[5].item() == 1.0
 
 
+@pytest.mark.parametrize("layout", ["paired", "native", "token_major"])
+@pytest.mark.parametrize("nb,bs,h,d,dtype", [(37, 16, 8, 128, torch.bfloat16), (5, 16, 4, 64, torch.float16),
+                                             (9, 8, 2, 32, torch.float32), (3, 16, 1, 128, torch.bfloat16)])
+def test_quantize_into_cache_layouts_bit_exact(gpu, layout, nb, bs, h, d, dtype):
+    """A pool quantized straight into each cache layout's K and V views
+    (token-major, tile-ordered and transposed writes) holds the oracle's
+    codes at every logical position."""
+    g = torch.Generator(device=gpu).manual_seed(nb * 1000 + d)
+    for is_v in (False, True):
+        x = (torch.randn(nb, bs, h, d, generator=g, device=gpu) * torch.logspace(-3, 2, h, device=gpu).view(1, 1, h, 1))
+        x = x.to(dtype)
+        scales = ops.fp8_amax_scale(x)
+        kc, vc = L.alloc_kv_cache(nb, bs, h, d, torch.float8_e4m3fn, gpu, layout)
+        dst = vc if is_v else kc
+        dst.view(torch.uint8).fill_(0xAA)
+        ops.fp8_quantize(x, scales, out=dst)
+        torch.cuda.synchronize()
+        want, _ = ofp8.quantize_per_head(x.float().cpu().numpy().reshape(-1, h, d))
+        assert np.array_equal(codes(dst.contiguous()).reshape(-1, h, d), want), (layout, is_v)
+
+
 def test_quantize_block_and_dequantize_bit_exact(gpu):
     quant = FP8KVCacheQuantizer(block_size=16)
     g = torch.Generator(device=gpu).manual_seed(2)
