@@ -159,21 +159,54 @@ struct Geo {
 };
 
 struct TileIds {
-  int a, b;     // physical blocks (block 0 stands in for an invalid id)
-  bool va, vb;  // ids valid
+  int a, b;  // physical blocks (block 0 stands in for an invalid id)
+  int ok;    // bit 0: a valid, bit 1: b valid
 };
 
-__device__ __forceinline__ TileIds tile_ids(const PrefillParams& p, const int32_t* __restrict__ tables, int n,
-                                            int j, int kvlen) {
+// Table entries -> ids; anything outside [0, NB) (including the -1 that
+// stands for a block past the item) is invalid.
+__device__ __forceinline__ TileIds tile_resolve(int ia, int ib, int NB) {
+  const bool va = (unsigned)ia < (unsigned)NB, vb = (unsigned)ib < (unsigned)NB;
   TileIds t;
-  const int nblk = (kvlen + 15) >> 4;
-  const int ia = tables[(int64_t)n * p.t_sb + (int64_t)(2 * j) * p.t_sm];
-  const int ib = 2 * j + 1 < nblk ? tables[(int64_t)n * p.t_sb + (int64_t)(2 * j + 1) * p.t_sm] : -1;
-  t.va = ia >= 0 && ia < p.NB;
-  t.vb = ib >= 0 && ib < p.NB;
-  t.a = t.va ? ia : 0;
-  t.b = t.vb ? ib : 0;
+  t.a = va ? ia : 0;
+  t.b = vb ? ib : 0;
+  t.ok = (va ? 1 : 0) | (vb ? 2 : 0);
   return t;
+}
+
+// Block ids of tile j from the item's table row (`trow`, stride t_sm).
+__device__ __forceinline__ TileIds tile_ids(const PrefillParams& p, const int32_t* __restrict__ trow, int j,
+                                            int kvlen) {
+  const int nblk = (kvlen + 15) >> 4;
+  const int ia = trow[(int64_t)(2 * j) * p.t_sm];
+  const int ib = 2 * j + 1 < nblk ? trow[(int64_t)(2 * j + 1) * p.t_sm] : -1;
+  return tile_resolve(ia, ib, p.NB);
+}
+
+// K piece u of a tile: 16 bytes of one token row.  X = block of the tile
+// (each wave's pieces come from one block, so its load addresses are one
+// scalar base plus a per-lane offset), s = chain, cp = 16-byte part of the
+// lane's D / 4 channels, (li, lq) = the lane it feeds.  The row pair index
+// runs fastest, so 8 consecutive threads write 8 consecutive LDS entries.
+struct KPiece {
+  int X, s, cp, li, lq, row;
+};
+
+template <int KT, int D>
+__device__ __forceinline__ KPiece k_piece(int u) {
+  using Gm = Geo<KT, D>;
+  constexpr int PB = 64 * Gm::KUPL;  // pieces per block
+  KPiece q;
+  q.X = u / PB;
+  const int idx = u % PB;
+  const int l8 = idx & 7;
+  q.lq = (idx >> 3) & 3;
+  const int sc = idx >> 5;  // s * KUPL + cp
+  q.cp = sc % Gm::KUPL;
+  q.s = sc / Gm::KUPL;
+  q.li = l8 + 8 * q.X;
+  q.row = (l8 & 3) + 8 * (l8 >> 2) + 4 * q.s;
+  return q;
 }
 
 // Global loads of one K/V tile into registers (16 bytes each).
@@ -187,14 +220,11 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
   for (int i = 0; i < Gm::KPT; ++i) {
     const int u = tid + 256 * i;
     if (Gm::KU % 256 == 0 || u < Gm::KU) {
-      const int s = u / (64 * Gm::KUPL), rem = u % (64 * Gm::KUPL);
-      const int lane = rem % 64, cp = rem / 64;
-      const int li = lane & 15, lq = lane >> 4;
-      const int row = ((8 * (li >> 2) + (li & 3)) & 15) + 4 * s;
-      const int blk = li < 8 ? t.a : t.b;
-      const int64_t off =
-          ((int64_t)blk * p.k_s[0] + (int64_t)h * p.k_s[2] + row * D + lq * (D / 4)) * Gm::KB + cp * 16;
-      kr[i] = *(const uint4*)(kbase + off);
+      const KPiece q = k_piece<KT, D>(u);
+      const int blk = uniform(q.X) ? t.b : t.a;
+      const uint8_t* b = kbase + ((int64_t)blk * p.k_s[0] + (int64_t)h * p.k_s[2]) * Gm::KB;
+      const uint32_t off = (uint32_t)((q.row * D + q.lq * (D / 4)) * Gm::KB + q.cp * 16);
+      kr[i] = *(const uint4*)(b + off);
     }
   }
 #pragma unroll
@@ -204,9 +234,10 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
       // 16 bytes of channel d of block X: all 16 tokens (e4m3) or half of them (bf16)
       const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
       const int d = rem / Gm::VPER, part = rem % Gm::VPER;
-      const int blk = X ? t.b : t.a;
-      const int64_t off = ((int64_t)blk * p.v_s[0] + (int64_t)h * p.v_s[2] + d * 16) * Gm::KB + part * 16;
-      vr[i] = *(const uint4*)(vbase + off);
+      const int blk = uniform(X) ? t.b : t.a;
+      const uint8_t* b = vbase + ((int64_t)blk * p.v_s[0] + (int64_t)h * p.v_s[2]) * Gm::KB;
+      const uint32_t off = (uint32_t)(d * 16 * Gm::KB + part * 16);
+      vr[i] = *(const uint4*)(b + off);
     }
   }
 }
@@ -225,8 +256,8 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
   for (int i = 0; i < Gm::KPT; ++i) {
     const int u = tid + 256 * i;
     if (Gm::KU % 256 == 0 || u < Gm::KU) {
-      const int s = u / (64 * Gm::KUPL), rem = u % (64 * Gm::KUPL);
-      const int lane = rem % 64, cp = rem / 64;
+      const KPiece q = k_piece<KT, D>(u);
+      const int s = q.s, cp = q.cp, lane = q.li + 16 * q.lq;
       if constexpr (KT == kE4M3) {
         lds[(s * Gm::NC + 2 * cp) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_bf16(kr[i].x, kr[i].y));
         lds[(s * Gm::NC + 2 * cp + 1) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_bf16(kr[i].z, kr[i].w));
@@ -238,14 +269,14 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
   uint4* vl = lds + Gm::KENT;
   // Tiles whose 32 tokens are all valid (all but an item's last tile) skip
   // the masking (a wave-uniform branch).
-  const bool full = FULL || (valid >= 32 && t.va && t.vb);
+  const bool full = FULL || (valid >= 32 && t.ok == 3);
 #pragma unroll
   for (int i = 0; i < Gm::VPT; ++i) {
     const int u = tid + 256 * i;
     if (Gm::VU % 256 == 0 || u < Gm::VU) {
       const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
       const int d = rem / Gm::VPER, part = rem % Gm::VPER;
-      const bool ok = X ? t.vb : t.va;
+      const bool ok = (t.ok >> X) & 1;
       const int li = d & 15, tt = d >> 4;
       if (full) {
         if constexpr (KT == kE4M3) {
@@ -280,7 +311,7 @@ __device__ __forceinline__ void mask_staged_v(uint4* vr, const TileIds& t, int v
     if (Gm::VU % 256 == 0 || u < Gm::VU) {
       const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
       const int part = rem % Gm::VPER;
-      const bool ok = X ? t.vb : t.va;
+      const bool ok = (t.ok >> X) & 1;
       if constexpr (KT == kE4M3) {
         const int n0 = ok ? valid - 16 * X : 0;
         const uint2 lo = keep_bytes(make_uint2(vr[i].x, vr[i].y), n0);
@@ -344,6 +375,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) lmin = min(lmin, __shfl_xor(lmin, o, 64));
     lmin = uniform(lmin);
+    const int lmin_t = lmin >> 5;  // tiles before the first one some column of the wave cannot see whole
     float qk_scale = p.scale * (kscale ? kscale[h * p.ks_s] : 1.0f) * kLog2e;
     if (qk_scale < 0.0f) {
       // the softmax takes its max on raw scores: keep the scale positive by
@@ -384,9 +416,13 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     // item's last tile the ids repeat the last valid ones: the extra load
     // reads real blocks and is never used.
     uint4 kr[Gm::KPT], vr[Gm::VPT];
-    TileIds id0 = tile_ids(p, tables, n, 0, kvlen);
-    TileIds id1 = nt > 1 ? tile_ids(p, tables, n, 1, kvlen) : id0;
-    TileIds id2 = nt > 2 ? tile_ids(p, tables, n, 2, kvlen) : id1;
+    const int32_t* trow = tables + (int64_t)n * p.t_sb;
+    const int nblk = (kvlen + 15) >> 4, nfull = kvlen >> 5;
+    const int64_t tsm = p.t_sm;
+    const int32_t* tp = trow + 6 * tsm;  // table entry of tile 3's first block, advanced every step
+    TileIds id0 = tile_ids(p, trow, 0, kvlen);
+    TileIds id1 = nt > 1 ? tile_ids(p, trow, 1, kvlen) : id0;
+    TileIds id2 = nt > 2 ? tile_ids(p, trow, 2, kvlen) : id1;
     if (nt > 0) {
       stage_load<KT, D>(kr, vr, p, id0, h, tid);
       stage_write<KT, D>(lds[0], kr, vr, id0, kvlen, tid);
@@ -412,8 +448,9 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     };
     // Scores column tile k may not see (edge tiles only) become -inf, in
     // place.
-    auto mask = [&](auto kc, f32x4_t& s1, f32x4_t& s2, bool blk_ok, int tok0) {
+    auto mask = [&](auto kc, f32x4_t& s1, f32x4_t& s2, int ok, int tok0) {
       constexpr int k = decltype(kc)::value;
+      const bool blk_ok = (ok >> (lq >> 1)) & 1;  // lanes lq 0-1 read block a, 2-3 block b
       const int nvalid = blk_ok ? lim[k] - tok0 : 0;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -422,11 +459,16 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       }
     };
     // The lane's max of column tile k's scaled scores (qk_scale > 0: the
-    // max of the scaled scores, in log2 units).
+    // max of the scaled scores, in log2 units).  NaN-propagating maximum
+    // (three-input v_maximum3 on gfx950, no canonicalizing of the MFMA
+    // results): it equals fmaxf whenever no score is NaN, and a NaN score
+    // makes the column's output NaN either way.
     auto lane_max = [&](const f32x4_t& s1, const f32x4_t& s2) {
-      float mt = fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]));
-      mt = fmaxf(mt, fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3])));
-      return mt * qk_scale;
+      const float m1 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(s1[0], s1[1]),
+                                                     __builtin_elementwise_maximum(s1[2], s1[3]));
+      const float m2 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(s2[0], s2[1]),
+                                                     __builtin_elementwise_maximum(s2[2], s2[3]));
+      return __builtin_elementwise_maximum(m1, m2) * qk_scale;
     };
     // The lazy rescale of column tile k: the running max moves only when a
     // score passes it by more than 8, so p <= 256.  The caller's lane-local
@@ -501,8 +543,14 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     auto step = [&](auto par, int j) {
       constexpr int P = decltype(par)::value;
       const int valid_next = kvlen - 32 * (j + 1);
-      if (!(valid_next >= 32 && id1.va && id1.vb)) mask_staged_v<KT, D>(vr, id1, valid_next, tid);
-      const TileIds id3 = j + 3 < nt ? tile_ids(p, tables, n, j + 3, kvlen) : id2;
+      if (!(j + 2 <= nfull && id1.ok == 3)) mask_staged_v<KT, D>(vr, id1, valid_next, tid);
+      // table entries of tile j + 3, read now and resolved after the math
+      int raw_a = -1, raw_b = -1;
+      if (j + 3 < nt) {
+        raw_a = tp[0];
+        if (2 * (j + 3) + 1 < nblk) raw_b = tp[tsm];
+      }
+      tp += 2 * tsm;
       const uint4* kl = lds[P];
       const uint4* vl = kl + Gm::KENT;
       bf16x8_t a1[NC], a2[NC];
@@ -512,8 +560,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
         a1[c] = as_bf16x8(kl[c * 64 + lane]);
         a2[c] = as_bf16x8(kl[(NC + c) * 64 + lane]);
       }
-      const bool edge = 32 * j + 32 > lmin || !id0.va || !id0.vb;
-      const bool blk_ok = lq < 2 ? id0.va : id0.vb;
+      const bool edge = j >= lmin_t || id0.ok != 3;
       const int tok0 = 32 * j + 8 * lq;
       constexpr auto K0 = std::integral_constant<int, 0>{};
       constexpr auto K1 = std::integral_constant<int, 1>{};
@@ -531,21 +578,24 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x020, Gm::KPT + Gm::VPT, 0);
-      if (edge) mask(K0, s1a, s2a, blk_ok, tok0);
+      if (edge) mask(K0, s1a, s2a, id0.ok, tok0);
       // QK^T of column tile 1 beside column tile 0's max; the V operands
       // are read from LDS meanwhile (not earlier: fewer registers live
       // across the QK^T products)
       qk(K1, a1, a2, s1b, s2b);
-      const float mta = lane_max(s1a, s2a);
 #pragma unroll
       for (int t = 0; t < NV; ++t) vraw[t] = vl[t * 64 + lane];
+      const float mta = lane_max(s1a, s2a);
+      // keeps the max here, beside the MFMAs, instead of sunk past the
+      // next branch to its use
+      asm volatile("" ::"v"(mta));
 #pragma unroll
       for (int i = 0; i < kQkMfma; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
         __builtin_amdgcn_sched_group_barrier(0x100, NV / kQkMfma > 0 ? NV / kQkMfma : 1, 1);
         __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);
       }
-      if (edge) mask(K1, s1b, s2b, blk_ok, tok0);
+      if (edge) mask(K1, s1b, s2b, id0.ok, tok0);
       const float mtb = lane_max(s1b, s2b);
       const bool up_a = mta > m[0] + 8.0f, up_b = mtb > m[1] + 8.0f;
       if (__any(up_a || up_b)) {
@@ -565,6 +615,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 2);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, kPvMfma, 2);
+      const TileIds id3 = j + 3 < nt ? tile_resolve(raw_a, raw_b, p.NB) : id2;
       __syncthreads();
       id0 = id1;
       id1 = id2;
