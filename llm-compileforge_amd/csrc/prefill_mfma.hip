@@ -610,11 +610,10 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       pv(K1, vraw, pb, plb);
       __builtin_amdgcn_sched_group_barrier(0x002, 20, 2);
 #pragma unroll
-      for (int i = 0; i < kPvMfma; ++i) {
+      for (int i = 0; i < 2 * kPvMfma; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 2);
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 2);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, kPvMfma, 2);
       const TileIds id3 = j + 3 < nt ? tile_resolve(raw_a, raw_b, p.NB) : id2;
       __syncthreads();
       id0 = id1;
