@@ -240,6 +240,22 @@ int32_t cf_kv_amax_scale(const CfTensor* x, CfTensor* scales_out, void* stream);
 int32_t cf_fp8_quantize(const CfTensor* x, const CfTensor* scales,
                         CfTensor* out, void* stream);
 
+/* k_out = e4m3fn(k / k_scales[h]) and v_out = e4m3fn(v / v_scales[h]) in
+ * one call: the reference's FP8KVCacheQuantizer.quantize_kv (independent K
+ * and V scales, compiler/quantize/fp8_kv_cache.py:107-122) quantizing
+ * straight into cache storage.
+ *   k, v [S0,S1,H,Dx] (or [T,H,Dx]) f32|f16|bf16, same dtype and shape;
+ *   k_scales, v_scales [H] or [1] f32; k_out, v_out e4m3fn, same shape.
+ * Codes equal cf_fp8_quantize's for each tensor.  When k, v are [S0,16,H,D]
+ * pools with 16-byte rows and the outputs are native-tile K / V views (K
+ * rows D bytes apart, V 16-token channel rows, shared block and head strides:
+ * the native and paired cache layouts) both are written by one launch, a
+ * workgroup per block writing every (block, head) pair whole; otherwise it
+ * runs cf_fp8_quantize on each. */
+int32_t cf_fp8_quantize_kv(const CfTensor* k, const CfTensor* v,
+                           const CfTensor* k_scales, const CfTensor* v_scales,
+                           CfTensor* k_out, CfTensor* v_out, void* stream);
+
 /* out[t,h,d] = f32(q[t,h,d]) * scales[h].
  * Reference compiler/quantize/fp8_kv_cache.py:95-105.
  *   q [T,H,Dx] or [S0,S1,H,Dx] e4m3fn; scales [H] or [1] f32;

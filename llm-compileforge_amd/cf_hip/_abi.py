@@ -164,6 +164,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "cf_fp8_amax_scale": (ctypes.c_int32, [_P, _P, ctypes.c_void_p]),
     "cf_kv_amax_scale": (ctypes.c_int32, [_P, _P, ctypes.c_void_p]),
     "cf_fp8_quantize": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
+    "cf_fp8_quantize_kv": (ctypes.c_int32, [_P, _P, _P, _P, _P, _P, ctypes.c_void_p]),
     "cf_fp8_dequantize": (ctypes.c_int32, [_P, _P, _P, ctypes.c_void_p]),
     "cf_kv_write_fp8": (ctypes.c_int32, [_P, _P, _P, _P, _P, _P, _P, ctypes.c_void_p]),
     "cf_paged_write": (ctypes.c_int32, [_P, _P, _P, _P, ctypes.c_void_p]),

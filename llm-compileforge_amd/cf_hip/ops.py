@@ -360,6 +360,28 @@ def fp8_quantize(x: torch.Tensor, scales: torch.Tensor, out: torch.Tensor | None
     return out
 
 
+def fp8_quantize_kv(k: torch.Tensor, v: torch.Tensor, k_scales: torch.Tensor, v_scales: torch.Tensor,
+                    k_out: torch.Tensor | None = None, v_out: torch.Tensor | None = None
+                    ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(e4m3fn(k / k_scales[h]), e4m3fn(v / v_scales[h])), the codes of two
+    fp8_quantize calls; one launch when k_out / v_out are a cache's native or
+    paired K / V views of [S0, 16, H, D] pools."""
+    for name, t in (("k", k), ("v", v), ("k_scales", k_scales), ("v_scales", v_scales)):
+        _require_device(name, t)
+    if k_out is None:
+        k_out = torch.empty(k.shape, dtype=torch.float8_e4m3fn, device=k.device)
+    if v_out is None:
+        v_out = torch.empty(v.shape, dtype=torch.float8_e4m3fn, device=v.device)
+    dk, dv = descriptor(_as3(k)), descriptor(_as3(v))
+    dks, dvs = descriptor(k_scales.reshape(-1)), descriptor(v_scales.reshape(-1))
+    dko, dvo = descriptor(_as3(k_out)), descriptor(_as3(v_out))
+    with torch.cuda.device(k.device):
+        rc = lib().cf_fp8_quantize_kv(ref(dk), ref(dv), ref(dks), ref(dvs), ref(dko), ref(dvo),
+                                      stream_handle(k.device))
+    check(rc, "cf_fp8_quantize_kv")
+    return k_out, v_out
+
+
 def fp8_dequantize(q: torch.Tensor, scales: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """f32(q) * scales[h]."""
     _require_device("q", q)
@@ -585,6 +607,7 @@ __all__ = [
     "fp8_amax_scale",
     "fp8_dequantize",
     "fp8_quantize",
+    "fp8_quantize_kv",
     "kv_write_fp8",
     "paged_decode",
     "paged_decode_noalloc",

@@ -185,8 +185,7 @@ def materialize(case: DecodeCase, layout: str = "paired"):
         k_scale = ops.fp8_amax_scale(case.k)
         v_scale = ops.fp8_amax_scale(case.v)
         kc, vc = _layout.alloc_kv_cache(nb, bs, hkv, d, torch.float8_e4m3fn, dev, layout)
-        ops.fp8_quantize(case.k, k_scale, out=kc)
-        ops.fp8_quantize(case.v, v_scale, out=vc)
+        ops.fp8_quantize_kv(case.k, case.v, k_scale, v_scale, kc, vc)
         return kc, vc, k_scale, v_scale
     kc, vc = _layout.alloc_kv_cache(nb, bs, hkv, d, case.kv_dtype, dev, layout)
     kc.copy_(case.k)
@@ -334,8 +333,7 @@ def materialize_mixed(case: MixedCase, layout: str = "paired") -> dict[str, torc
         ks = torch.maximum(ops.fp8_amax_scale(case.k_pool), ops.fp8_amax_scale(case.k_new))
         vs = torch.maximum(ops.fp8_amax_scale(case.v_pool), ops.fp8_amax_scale(case.v_new))
         kc, vc = _layout.alloc_kv_cache(nb, bs, hkv, d, torch.float8_e4m3fn, dev, layout)
-        ops.fp8_quantize(case.k_pool, ks, out=kc)
-        ops.fp8_quantize(case.v_pool, vs, out=vc)
+        ops.fp8_quantize_kv(case.k_pool, case.v_pool, ks, vs, kc, vc)
         t.update(k_scale=ks, v_scale=vs)
     else:
         kc, vc = _layout.alloc_kv_cache(nb, bs, hkv, d, case.kv_dtype, dev, layout)

@@ -607,6 +607,29 @@ int32_t cf_fp8_quantize(const CfTensor* x, const CfTensor* scales, CfTensor* out
   return launch_quantize(x4, vx.dtype, sp, ss, o4, as_stream(stream));
 }
 
+int32_t cf_fp8_quantize_kv(const CfTensor* k, const CfTensor* v, const CfTensor* k_scales, const CfTensor* v_scales,
+                           CfTensor* k_out, CfTensor* v_out, void* stream) {
+  View vk, vv, vko, vvo;
+  int32_t rc;
+  if ((rc = view_of_34(k, "k", &vk))) return rc;
+  if ((rc = view_of_34(v, "v", &vv))) return rc;
+  if ((rc = view_of_34(k_out, "k_out", &vko))) return rc;
+  if ((rc = view_of_34(v_out, "v_out", &vvo))) return rc;
+  CF_CHECK(is_float_dtype(vk.dtype), "k: dtype must be f32, f16 or bf16, got %s", dtype_name(vk.dtype));
+  CF_CHECK(vv.dtype == vk.dtype, "v: dtype %s differs from k's %s", dtype_name(vv.dtype), dtype_name(vk.dtype));
+  CF_CHECK(vko.dtype == CF_F8E4M3FN && vvo.dtype == CF_F8E4M3FN, "k_out, v_out: expected f8e4m3fn");
+  const Rank4 k4 = rank4_of(vk), v4 = rank4_of(vv), ko4 = rank4_of(vko), vo4 = rank4_of(vvo);
+  for (int i = 0; i < 4; ++i) {
+    CF_CHECK(v4.size[i] == k4.size[i], "v shape differs from k");
+    CF_CHECK(ko4.size[i] == k4.size[i] && vo4.size[i] == k4.size[i], "output shapes differ from k");
+  }
+  const float *ksp, *vsp;
+  int64_t kss, vss;
+  if ((rc = scale_view(k_scales, "k_scales", k4.size[2], &ksp, &kss))) return rc;
+  if ((rc = scale_view(v_scales, "v_scales", k4.size[2], &vsp, &vss))) return rc;
+  return launch_quantize_kv(k4, v4, vk.dtype, ksp, kss, vsp, vss, ko4, vo4, as_stream(stream));
+}
+
 int32_t cf_fp8_dequantize(const CfTensor* q, const CfTensor* scales, CfTensor* out, void* stream) {
   View vq, vo;
   int32_t rc;

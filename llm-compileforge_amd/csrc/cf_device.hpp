@@ -64,7 +64,9 @@ __device__ __forceinline__ uint8_t e4m3_from_f32(float f) {
 struct Fp8Quant {
   float s, r;
   bool fast;
-  __device__ __forceinline__ explicit Fp8Quant(float scale) : s(scale), r(1.0f / scale) {
+  __device__ __forceinline__ explicit Fp8Quant(float scale) : Fp8Quant(scale, 1.0f / scale) {}
+  // `recip` must be fl(1 / scale) (computed once per head by the caller).
+  __device__ __forceinline__ Fp8Quant(float scale, float recip) : s(scale), r(recip) {
     const uint32_t es = (f2u(scale) >> 23) & 0x1FFu;  // sign + exponent
     const uint32_t er = (f2u(r) >> 23) & 0x1FFu;
     fast = es != 0u && es < 0xFFu && er != 0u && er < 0xFFu;

@@ -32,6 +32,10 @@ struct KvWriteParams {
 int32_t launch_amax_scale(const Rank4& x, int x_dt, float* scales, int64_t s_stride, hipStream_t stream);
 int32_t launch_quantize(const Rank4& x, int x_dt, const float* scales, int64_t s_stride, const Rank4& out,
                         hipStream_t stream);
+// K and V with their own per-head scales; one launch when the outputs are
+// native-tile (e.g. paired) K and V views of [S0, 16, H, D] pools.
+int32_t launch_quantize_kv(const Rank4& k, const Rank4& v, int x_dt, const float* ks, int64_t ks_s, const float* vs,
+                           int64_t vs_s, const Rank4& ko, const Rank4& vo, hipStream_t stream);
 int32_t launch_dequantize(const Rank4& q, const float* scales, int64_t s_stride, const Rank4& out,
                           hipStream_t stream);
 int32_t launch_kv_write_fp8(const KvWriteParams& p, int x_dt, int slot_dt, hipStream_t stream);

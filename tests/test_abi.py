@@ -233,6 +233,21 @@ def test_fp8_entry_points_validate():
     s2.t.device = _abi.SFA_ROCM
     assert lib.cf_fp8_quantize(_abi.ref(x), _abi.ref(s2), _abi.ref(o), None) == _abi.CF_ERR_INVALID
     assert "f8e4m3fn" in _abi.last_error()
+    # fused K + V: dtype and shape mismatches are refused before any launch
+    v = _abi.descriptor(torch.zeros(4, 2, 8, dtype=torch.float16))
+    v.t.device = _abi.SFA_ROCM
+    assert lib.cf_fp8_quantize_kv(_abi.ref(x), _abi.ref(v), _abi.ref(s2), _abi.ref(s2), _abi.ref(o), _abi.ref(o),
+                                  None) == _abi.CF_ERR_INVALID
+    assert "differs from k" in _abi.last_error()
+    v = _abi.descriptor(torch.zeros(4, 2, 16))
+    o8 = _abi.descriptor(torch.zeros(4, 2, 8, dtype=torch.float8_e4m3fn))
+    v.t.device = o8.t.device = _abi.SFA_ROCM
+    assert lib.cf_fp8_quantize_kv(_abi.ref(x), _abi.ref(v), _abi.ref(s2), _abi.ref(s2), _abi.ref(o8), _abi.ref(o8),
+                                  None) == _abi.CF_ERR_INVALID
+    assert "v shape differs" in _abi.last_error()
+    assert lib.cf_fp8_quantize_kv(_abi.ref(x), _abi.ref(x), _abi.ref(s2), _abi.ref(s2), _abi.ref(o8), _abi.ref(o),
+                                  None) == _abi.CF_ERR_INVALID
+    assert "f8e4m3fn" in _abi.last_error()
 
 
 def test_last_error_truncates_safely():

@@ -106,6 +106,66 @@ def test_quantize_into_cache_layouts_bit_exact(gpu, layout, nb, bs, h, d, dtype)
         assert np.array_equal(codes(dst.contiguous()).reshape(-1, h, d), want), (layout, is_v)
 
 
+@pytest.mark.parametrize("layout", ["paired", "native", "token_major"])
+@pytest.mark.parametrize("nb,h,d,dtype", [(41, 8, 128, torch.bfloat16), (7, 4, 64, torch.float16),
+                                          (5, 2, 80, torch.float32), (3, 1, 128, torch.bfloat16),
+                                          (2, 16, 32, torch.bfloat16)])
+def test_quantize_kv_into_cache_layouts_bit_exact(gpu, layout, nb, h, d, dtype):
+    """fp8_quantize_kv (one launch on native / paired tiles, two otherwise)
+    writes, for K and V with their own per-head scales, the oracle's codes at
+    every logical position -- the same codes as fp8_quantize on each."""
+    g = torch.Generator(device=gpu).manual_seed(nb * 7 + d)
+    mag = torch.logspace(-4, 3, h, device=gpu).view(1, 1, h, 1)
+    k = (torch.randn(nb, 16, h, d, generator=g, device=gpu) * mag).to(dtype)
+    v = (torch.randn(nb, 16, h, d, generator=g, device=gpu) * mag.flip(2)).to(dtype)
+    v[:, :, 0] = 0.0  # an all-zero head: scale 1.0
+    ks, vs = ops.fp8_amax_scale(k), ops.fp8_amax_scale(v)
+    kc, vc = L.alloc_kv_cache(nb, 16, h, d, torch.float8_e4m3fn, gpu, layout)
+    kc.view(torch.uint8).fill_(0x55)
+    vc.view(torch.uint8).fill_(0x55)
+    ops.fp8_quantize_kv(k, v, ks, vs, kc, vc)
+    torch.cuda.synchronize()
+    for x, sc, out in ((k, ks, kc), (v, vs, vc)):
+        want, want_s = ofp8.quantize_per_head(x.float().cpu().numpy().reshape(-1, h, d))
+        assert np.array_equal(sc.cpu().numpy().view(np.uint32), want_s.view(np.uint32))
+        assert np.array_equal(codes(out).reshape(-1, h, d), want), layout
+        assert torch.equal(out.contiguous().view(torch.uint8), ops.fp8_quantize(x, sc).view(torch.uint8))
+
+
+def test_quantize_kv_strided_inputs_and_extreme_scales(gpu):
+    """Inputs that are views with gaps between rows, and scales at the edges
+    of the fp32 range (reciprocals that are not normal take the division),
+    give the per-tensor codes; a block size other than 16 takes two launches."""
+    g = torch.Generator(device=gpu).manual_seed(3)
+    big = torch.randn(6, 16, 4, 160, generator=g, device=gpu).to(torch.bfloat16)
+    k, v = big[..., :128], big[..., 32:]          # rows 320 bytes apart, V at a 64-byte offset
+    kc, vc = L.alloc_kv_cache(6, 16, 4, 128, torch.float8_e4m3fn, gpu, "paired")
+    for ks in (torch.tensor([1e-12, 3e38, 1.0, 2.0 ** -126], device=gpu),
+               torch.tensor([0.75, 1e-30, 448.0, 5e-39], device=gpu)):
+        vs = ks.flip(0).contiguous()
+        ops.fp8_quantize_kv(k, v, ks, vs, kc, vc)
+        torch.cuda.synchronize()
+        assert torch.equal(kc.contiguous().view(torch.uint8), ops.fp8_quantize(k, ks).view(torch.uint8))
+        assert torch.equal(vc.contiguous().view(torch.uint8), ops.fp8_quantize(v, vs).view(torch.uint8))
+        # the oracle with the scales given
+        want = np.stack([ofp8.quantize(k[:, :, i].float().cpu().numpy(), np.float32(ks[i].item()))
+                         for i in range(4)], axis=2).reshape(-1, 4, 128)
+        assert np.array_equal(codes(kc).reshape(-1, 4, 128), want)
+    # the one-launch shape with the same extreme scales
+    k2, v2 = k.contiguous(), v.contiguous()
+    ks = torch.tensor([1e-12, 3e38, 1.0, 2.0 ** -126], device=gpu)
+    ops.fp8_quantize_kv(k2, v2, ks, ks, kc, vc)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.contiguous().view(torch.uint8), ops.fp8_quantize(k2, ks).view(torch.uint8))
+    assert torch.equal(vc.contiguous().view(torch.uint8), ops.fp8_quantize(v2, ks).view(torch.uint8))
+    k8, v8 = k2.reshape(12, 8, 4, 128), v2.reshape(12, 8, 4, 128)
+    kc8, vc8 = L.alloc_kv_cache(12, 8, 4, 128, torch.float8_e4m3fn, gpu, "paired")
+    ops.fp8_quantize_kv(k8, v8, ks, ks, kc8, vc8)
+    torch.cuda.synchronize()
+    assert torch.equal(kc8.contiguous().view(torch.uint8), ops.fp8_quantize(k8, ks).view(torch.uint8))
+    assert torch.equal(vc8.contiguous().view(torch.uint8), ops.fp8_quantize(v8, ks).view(torch.uint8))
+
+
 def test_quantize_block_and_dequantize_bit_exact(gpu):
     quant = FP8KVCacheQuantizer(block_size=16)
     g = torch.Generator(device=gpu).manual_seed(2)
