@@ -19,8 +19,12 @@
 // both exact) and written to LDS in MFMA operand order: an LDS entry is the
 // 16 bytes one lane feeds one MFMA, entries of one MFMA are consecutive, so
 // every operand read is a conflict-free ds_read_b128.  Two LDS buffers and
-// two register stages: while tile j is computed from LDS, tile j + 1 goes
-// from registers to the other buffer and tile j + 2 is loading.
+// one register stage: in step j the registers holding tile j + 1 go to the
+// free buffer and tile j + 2 starts loading into them, while tile j is
+// computed from the other buffer.  Each staging wave reads one block, so
+// its load addresses are a scalar block base plus a per-lane offset; the
+// row pair index runs fastest, so 8 consecutive threads write 8
+// consecutive LDS entries (no bank conflicts).
 //
 // Per tile and column tile the math is the decode kernel's (decode_mfma.hip):
 // S^T = K Q^T as two 16-token MFMA chains, online softmax in log2 units
@@ -30,8 +34,14 @@
 // (a column's max across its 4 lanes is taken only when some lane passes
 // the threshold), and the row sums come out of the MFMA pipe as one more
 // PV product against an all-ones V channel instead of per-score adds.
-// Staging threads take K operand entries lane-fastest so the LDS writes of
-// a wave are contiguous (no bank conflicts).
+//
+// A wave issues in order, one instruction per four cycles at most, so its
+// MFMAs overlap VALU work only when the two are interleaved in its own
+// instruction stream.  Each step is laid out in phases that give every
+// batch of MFMAs independent VALU work (sched_group_barrier pins the
+// interleave): column tile 0's QK^T beside the staging conversion, column
+// tile 1's QK^T beside column tile 0's max, one lazy-rescale branch for
+// both column tiles, then both P.V products beside the exponentials.
 //
 // Items come from a queue the plan kernel sorts longest first (counting
 // sort on the tile count), so the persistent workgroups finish together
