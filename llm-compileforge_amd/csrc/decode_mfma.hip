@@ -538,7 +538,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   const KvCacheView kv{(const uint8_t*)p.k, (const uint8_t*)p.v, p.k_s[0], p.k_s[2], p.v_s[0], p.v_s[2],
                        p.k_s[1], p.v_s[1]};
   // token-major V: this wave's LDS staging rows, after the plan
-  uint8_t* vstage = (uint8_t*)dyn_lds + (PL ? kPlanLdsBytes : 0) + wave * vtok_stage_bytes<D>();
+  uint8_t* vstage = (uint8_t*)dyn_lds + (PL ? kPlanLdsBytes : 0) + wave * vtok_stage_bytes<D, KvTraits<KT>::kBytes>();
   (void)vstage;
   TileRegs<KT, D, VTOK> r0, r1;
   load_tile<KT, D, VTOK>(r0, kv, c0.blkA, c0.blkB, li, lq, c0.h, lane);
@@ -591,17 +591,20 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     using VT = typename TileRegs<KT, D, VTOK>::VT;
     VT vraw[NV];
     if constexpr (VTOK) {
-      static_assert(KT == kE4M3, "token-major V: e4m3 caches only");
+      constexpr int KB = KvTraits<KT>::kBytes;
       // the previous tile's transposed reads are done before its rows are overwritten
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      vtok_stage<D>(vstage, r0.v, lane);
+      vtok_stage<D, KB>(vstage, r0.v, lane);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int t = 0; t < NV; ++t) vraw[t] = vtok_operand<D>(vstage, t, li, lq);
+      for (int t = 0; t < NV; ++t) {
+        if constexpr (KB == 1) vraw[t] = vtok_operand<D>(vstage, t, li, lq);
+        else vraw[t] = vtok_operand16<D>(vstage, t, li, lq);
+      }
     } else {
 #pragma unroll
       for (int t = 0; t < NV; ++t) vraw[t] = r0.v[t];
@@ -932,9 +935,9 @@ int cu_count() {
 // Llama-3-8B shape).  The workspace holds slots for this many waves.
 constexpr int kStreamBlocksPerCU = 1;
 
-template <int D, bool PL, bool VTOK>
+template <int KT, int D, bool PL, bool VTOK>
 constexpr size_t stream_lds_bytes() {
-  return (PL ? kPlanLdsBytes : 0) + (VTOK ? 4 * (size_t)vtok_stage_bytes<D>() : 0);
+  return (PL ? kPlanLdsBytes : 0) + (VTOK ? 4 * (size_t)vtok_stage_bytes<D, KvTraits<KT>::kBytes>() : 0);
 }
 
 template <int QT, int KT, int D, bool PL, bool VTOK>
@@ -943,7 +946,7 @@ int blocks_per_cu() {
   if (cached == 0) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<QT, KT, D, PL, VTOK>, 256,
-                                                     stream_lds_bytes<D, PL, VTOK>()) != hipSuccess ||
+                                                     stream_lds_bytes<KT, D, PL, VTOK>()) != hipSuccess ||
         n < 1)
       n = 1;
     cached = n < kStreamBlocksPerCU ? n : kStreamBlocksPerCU;
@@ -955,7 +958,7 @@ template <int QT, int KT, int D, bool PL, bool VTOK>
 int32_t launch_stream_t(const DecodeParams& p, hipStream_t stream) {
   const int blocks = cu_count() * blocks_per_cu<QT, KT, D, PL, VTOK>();
   ProfileScope prof("cf_decode_mfma", stream);
-  CF_LAUNCH((decode_stream_kernel<QT, KT, D, PL, VTOK>), dim3(blocks), dim3(256), (stream_lds_bytes<D, PL, VTOK>()),
+  CF_LAUNCH((decode_stream_kernel<QT, KT, D, PL, VTOK>), dim3(blocks), dim3(256), (stream_lds_bytes<KT, D, PL, VTOK>()),
             stream, p, p.tables, p.seq_lens, p.k_scale, p.v_scale, PL ? p.shared : nullptr);
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
@@ -974,11 +977,7 @@ int32_t launch_pl(const DecodeParams& p, hipStream_t stream) {
 template <int QT, int KT, int D>
 int32_t launch_t(const DecodeParams& p, hipStream_t stream) {
   int32_t rc;
-  if constexpr (KT == kE4M3) {
-    rc = v_token_major(p) ? launch_pl<QT, KT, D, true>(p, stream) : launch_pl<QT, KT, D, false>(p, stream);
-  } else {
-    rc = launch_pl<QT, KT, D, false>(p, stream);
-  }
+  rc = v_token_major(p) ? launch_pl<QT, KT, D, true>(p, stream) : launch_pl<QT, KT, D, false>(p, stream);
   if (rc) return rc;
   const dim3 grid(p.Hkv, p.B);
   ProfileScope prof("cf_decode_merge", stream);
@@ -1046,12 +1045,12 @@ bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
   // K: token rows with unit channel stride, 16-byte aligned (token stride D
   // in the native / paired layouts, any multiple of 16 bytes token-major).
   // V: the native tile [D][bs] (token stride 1, channel stride bs), or
-  // token-major rows (channel stride 1; e4m3 only) -- block/head strides free.
+  // token-major rows (channel stride 1) -- block/head strides free.
   if (p.k_s[3] != 1) return false;
   for (int i = 0; i < 3; ++i)
     if ((p.k_s[i] * kb) % 16 != 0) return false;
   const bool v_native = p.v_s[1] == 1 && p.v_s[3] == 16;
-  const bool v_tok = kv_dt == kE4M3 && p.v_s[3] == 1 && p.v_s[1] != 1 && (p.v_s[1] * kb) % 16 == 0;
+  const bool v_tok = p.v_s[3] == 1 && p.v_s[1] != 1 && (p.v_s[1] * kb) % 16 == 0;
   if (!v_native && !v_tok) return false;
   // native V rides with the native K tile (token stride D)
   if (v_native && p.k_s[1] != p.D) return false;

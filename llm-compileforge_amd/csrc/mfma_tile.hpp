@@ -133,30 +133,36 @@ __device__ __forceinline__ void load_tile(TileRegs<KT, D, VTOK>& r, const KvCach
   }
 }
 
-// Token-major V, e4m3: the wave's LDS staging area holds the tile's 32 token
-// rows at kVtokRowStride bytes each (the row pieces exactly as loaded), and
-// ds_read_b64_tr_b8 returns the channel-major operand: within each group of
-// 16 lanes, lane L receives byte L % 8 of the 8-byte words supplied by lanes
-// 2j + L / 8 (j = 0..7).  Lane (li, lq) of PV step t therefore points lanes
-// 2j + b at token 8 lq + j, channels 16 t + 8 b .. + 7, and receives channel
-// 16 t + li of tokens 8 lq .. 8 lq + 7 -- the operand the native layout
-// loads straight from HBM.  The row stride's 16-byte pad keeps the 8 rows a
-// group reads in distinct banks.
-template <int D>
+// Token-major V: the wave's LDS staging area holds the tile's 32 token rows
+// of D elements (KB bytes each) at vtok_row_stride bytes apart -- the row
+// pieces exactly as loaded -- and the transposing LDS reads return the
+// channel-major operand the native layout loads straight from HBM.
+//  e4m3 (ds_read_b64_tr_b8): within each group of 16 lanes, lane L receives
+//   byte L % 8 of the 8-byte words supplied by lanes 2j + L / 8 (j = 0..7).
+//   Lane (li, lq) of PV step t points lanes 2j + b at token 8 lq + j,
+//   channels 16 t + 8 b .. + 7, and receives channel 16 t + li of tokens
+//   8 lq .. 8 lq + 7.
+//  16-bit (ds_read_b64_tr_b16): lane L receives element L % 4 of the 8-byte
+//   words (4 elements) supplied by lanes 4j + L / 4 (j = 0..3).  Two reads per
+//   operand: for tokens 8 lq + 4 h .. + 3, lane (li, lq) points at token
+//   8 lq + 4 h + li / 4, channels 16 t + 4 (li % 4) .. + 3, and receives
+//   channel 16 t + li of those four tokens.
+// The row stride's 16-byte pad spreads the rows a group reads over the banks.
+template <int D, int KB = 1>
 constexpr int vtok_row_stride() {
-  return D + 16;
+  return D * KB + 16;
 }
-template <int D>
+template <int D, int KB = 1>
 constexpr int vtok_stage_bytes() {
-  return 32 * vtok_row_stride<D>();
+  return 32 * vtok_row_stride<D, KB>();
 }
 
-template <int D>
+template <int D, int KB = 1>
 __device__ __forceinline__ void vtok_stage(uint8_t* stage, const uint4* v, int lane) {
-  constexpr int LPR = D / 16, RPI = 64 / LPR, NVR = 32 * D / (64 * 16);
+  constexpr int LPR = D * KB / 16, RPI = 64 / LPR, NVR = 32 * D * KB / (64 * 16);
 #pragma unroll
   for (int i = 0; i < NVR; ++i)
-    *(uint4*)(stage + (lane / LPR + RPI * i) * vtok_row_stride<D>() + (lane % LPR) * 16) = v[i];
+    *(uint4*)(stage + (lane / LPR + RPI * i) * vtok_row_stride<D, KB>() + (lane % LPR) * 16) = v[i];
 }
 
 typedef int v2i32_t __attribute__((ext_vector_type(2)));
@@ -167,6 +173,21 @@ __device__ __forceinline__ uint2 vtok_operand(const uint8_t* stage, int t, int l
   const v2i32_t r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
       (__attribute__((address_space(3))) v2i32_t*)((__attribute__((address_space(3))) const uint8_t*)src));
   return make_uint2((uint32_t)r.x, (uint32_t)r.y);
+}
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+
+// 16-bit V: channel 16 t + li of tokens 8 lq .. 8 lq + 7 (8 elements).
+template <int D>
+__device__ __forceinline__ uint4 vtok_operand16(const uint8_t* stage, int t, int li, int lq) {
+  constexpr int RS = vtok_row_stride<D, 2>();
+  const uint8_t* src = stage + (8 * lq + (li >> 2)) * RS + 32 * t + 8 * (li & 3);
+  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16_t*)((__attribute__((address_space(3))) const uint8_t*)src));
+  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16_t*)((__attribute__((address_space(3))) const uint8_t*)(src + 4 * RS)));
+  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+  return make_uint4(a.x, a.y, b.x, b.y);
 }
 
 // Keeps the first `nbytes` bytes of an 8-byte register pair, zeroing the rest.

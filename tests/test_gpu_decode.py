@@ -457,14 +457,17 @@ def test_full_c4_llama3_70b(gpu):
     assert torch.equal(out2, out)
 
 
+@pytest.mark.parametrize("kv_dtype,q_dtype", [(torch.float8_e4m3fn, torch.bfloat16), (torch.bfloat16, torch.bfloat16),
+                                              (torch.float16, torch.float16)])
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 2, 128), (32, 2, 64)])
-def test_token_major_fp8_on_the_mfma_path(gpu, hq, hkv, d):
-    """e4m3 caches in the reference's own token-major layout ([NB, bs, Hkv, D])
-    run the MFMA kernel (V staged through LDS and read back transposed);
-    lengths ending mid-block and mid-tile, one token, an invalid block id and
-    a shared-prefix statement; outputs bitwise equal to the native layout's
-    (the same operands reach the same MFMAs) and to the oracle's bound."""
-    print(f"[case] token-major e4m3 hq={hq} hkv={hkv} d={d}", flush=True)
+def test_token_major_on_the_mfma_path(gpu, hq, hkv, d, kv_dtype, q_dtype):
+    """Caches in the reference's own token-major layout ([NB, bs, Hkv, D]) run
+    the MFMA kernel (V staged through LDS and read back transposed: 8-bit
+    rows for e4m3, 16-bit for bf16 / fp16); lengths ending mid-block and
+    mid-tile, one token, an invalid block id and a shared-prefix statement;
+    outputs bitwise equal to the native layout's (the same operands reach
+    the same MFMAs) and to the oracle's bound."""
+    print(f"[case] token-major {kv_dtype} hq={hq} hkv={hkv} d={d}", flush=True)
     g = torch.Generator(device=gpu).manual_seed(hq + 7 * d)
     lens = [1, 15, 33, 700, 1024 + 40, 1024 + 100, 2000]
     nb = 400
@@ -479,10 +482,10 @@ def test_token_major_fp8_on_the_mfma_path(gpu, hq, hkv, d):
         else:
             tables.append(perm[pos:pos + k])
             pos += k
-    q = torch.randn(len(lens), hq, d, generator=g, device=gpu).to(torch.bfloat16)
-    ksrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
-    vsrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
-    case = workloads.DecodeCase("tok", q, ksrc, vsrc, tables, lens, 16, 1 / math.sqrt(d), torch.float8_e4m3fn)
+    q = torch.randn(len(lens), hq, d, generator=g, device=gpu).to(q_dtype)
+    ksrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(q_dtype)
+    vsrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(q_dtype)
+    case = workloads.DecodeCase("tok", q, ksrc, vsrc, tables, lens, 16, 1 / math.sqrt(d), kv_dtype)
     kt, vt, ks, vs = workloads.materialize(case, "token_major")
     assert L.layout_of(kt, False) == "token_major" and L.layout_of(vt, True) == "token_major"
     kn, vn, _, _ = workloads.materialize(case, "native")
@@ -502,7 +505,68 @@ def test_token_major_fp8_on_the_mfma_path(gpu, hq, hkv, d):
     eff = list(lens)
     eff[3] -= 16
     ref = oracle_decode(case, kt, vt, ks, vs, tables=tables[:3] + [t3] + tables[4:], lens=eff)
-    assert_close(out_t.float().cpu().numpy(), ref, torch.bfloat16, f"token-major {hq}/{hkv}/{d}")
+    assert_close(out_t.float().cpu().numpy(), ref, q_dtype, f"token-major {kv_dtype} {hq}/{hkv}/{d}")
+
+
+@pytest.mark.parametrize("kv_dtype,q_dtype", [(torch.float8_e4m3fn, torch.bfloat16), (torch.bfloat16, torch.bfloat16),
+                                              (torch.float16, torch.float16)])
+def test_head_major_tiles_on_the_mfma_path(gpu, kv_dtype, q_dtype):
+    """K and V both stored as [NB, {K, V}, Hkv, bs, D] (one (block, head) tile
+    of token rows per head, as the engine mixin's combined cache keeps a
+    layer): V is token-major with head stride bs*D, which the MFMA kernel
+    takes like the reference's layout; bitwise equal to the native layout."""
+    print(f"[case] head-major tiles {kv_dtype}", flush=True)
+    hq, hkv, d, nb = 32, 8, 128, 300
+    g = torch.Generator(device=gpu).manual_seed(11)
+    lens = [1, 17, 500, 1300, 2048]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(2)).tolist()
+    tables, pos = [], 0
+    for n in lens:
+        tables.append(perm[pos:pos + (n + 15) // 16])
+        pos += (n + 15) // 16
+    q = torch.randn(len(lens), hq, d, generator=g, device=gpu).to(q_dtype)
+    ksrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(q_dtype)
+    vsrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(q_dtype)
+    case = workloads.DecodeCase("hm", q, ksrc, vsrc, tables, lens, 16, 1 / math.sqrt(d), kv_dtype)
+    kn, vn, ks, vs = workloads.materialize(case, "native")
+    store = torch.empty(nb, 2, hkv, 16, d, dtype=kv_dtype, device=gpu)
+    kh, vh = store[:, 0].permute(0, 2, 1, 3), store[:, 1].permute(0, 2, 1, 3)
+    raw = (lambda t: t.view(torch.uint8)) if kv_dtype == torch.float8_e4m3fn else (lambda t: t)
+    raw(kh).copy_(raw(kn))
+    raw(vh).copy_(raw(vn))
+    assert vh.stride() == (2 * hkv * 16 * d, d, 16 * d, 1)
+    tab, sl = case.tables_tensor(gpu), case.seq_lens_tensor(gpu)
+    with ops.KernelTimer() as timer:
+        out_h = paged_attention_tensors(q, kh, vh, tab, sl, 16, case.scale, k_scale=ks, v_scale=vs)
+        out_n = paged_attention_tensors(q, kn, vn, tab, sl, 16, case.scale, k_scale=ks, v_scale=vs)
+        torch.cuda.synchronize()
+        assert timer.query("cf_decode_mfma")[1] == 2 and timer.query("cf_decode_generic")[1] == 0
+    assert torch.equal(out_h, out_n)
+    ref = oracle_decode(case, kn, vn, ks, vs)
+    assert_close(out_h.float().cpu().numpy(), ref, q_dtype, f"head-major {kv_dtype}")
+
+
+def test_full_c2_token_major(gpu):
+    """Config 2 (bf16 caches) in the reference's token-major layout at full
+    size: the MFMA path, bitwise equal to the paired layout's output, and the
+    oracle on sampled sequences."""
+    print("[case] c2 full size, token-major layout", flush=True)
+    case = workloads.make_case("c2_tinyllama", device=gpu, seed=0)
+    kt, vt, ks, vs = workloads.materialize(case, "token_major")
+    kp, vp, _, _ = workloads.materialize(case, "paired")
+    tables, lens = case.tables_tensor(gpu), case.seq_lens_tensor(gpu)
+    with ops.KernelTimer() as timer:
+        out_t = ops.DecodePlan(case.q, kt, vt, tables, lens, case.scale, 16, ks, vs).run()
+        torch.cuda.synchronize()
+        assert timer.query("cf_decode_mfma")[1] == 1 and timer.query("cf_decode_generic")[1] == 0
+    out_p = ops.DecodePlan(case.q, kp, vp, tables, lens, case.scale, 16, ks, vs).run()
+    torch.cuda.synchronize()
+    assert torch.equal(out_t, out_p)
+    idx = _sample_ids(case.seq_lens, [0, 1, 31], 13, seed=4)
+    sub = workloads.DecodeCase("c2_tok", case.q[idx], case.k, case.v, [case.block_tables[i] for i in idx],
+                               [case.seq_lens[i] for i in idx], 16, case.scale, case.kv_dtype)
+    ref = oracle_decode(sub, kt, vt, ks, vs)
+    assert_close(out_t[idx].float().cpu().numpy(), ref, torch.bfloat16, "c2 token-major")
 
 
 def test_full_c3_token_major(gpu):
