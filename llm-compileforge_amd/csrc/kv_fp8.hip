@@ -226,69 +226,118 @@ __device__ __forceinline__ int64_t slot_at(const KvWriteParams& p, int64_t i) {
 // K row piece.  Workgroups after that: V, one per (group of 16 new rows,
 // 256 channels of the H * D); each thread owns one (head, channel).  V is
 // channel-major in a block (16 tokens of a channel are 16 contiguous
-// bytes), so the rows are walked as runs of consecutive slots inside one
+// bytes), so the rows are split into runs of consecutive slots inside one
 // block: a run starting in the group is written by this workgroup (it may
 // extend past the group), a full block row as one 16-byte store, a partial
 // run as byte stores.  Run boundaries depend only on the slots, so every
-// thread of the workgroup walks the same runs.
+// thread of the workgroup writes the same runs.
+//
+// The kernel is bound by latency and instruction issue (a few microseconds
+// for a step's rows), not by bytes: loads of the new rows do not wait for
+// the slots, index math is 32-bit, and the per-row work of the V path is
+// vector code (one scalar unit serves the CU's four SIMDs).
 template <int XT, int ST>
-__global__ __launch_bounds__(256) void kv_write_native_kernel(KvWriteParams p, int64_t k_blocks, int v_chunks) {
+__global__ __launch_bounds__(256) void kv_write_native_kernel(KvWriteParams p, uint32_t k_blocks, uint32_t v_chunks) {
   using XE = Elem<XT>;
-  constexpr int EB = sizeof(typename XE::T);
-  if ((int64_t)blockIdx.x < k_blocks) {
-    const int nch = p.D / 16;
-    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (u >= p.T * p.H * nch) return;
-    const int c = (int)(u % nch), h = (int)((u / nch) % p.H);
-    const int64_t i = u / ((int64_t)nch * p.H);
+  using T = typename XE::T;
+  constexpr int EB = sizeof(T);
+  const int64_t cap = p.NB * 16;
+  if (blockIdx.x < k_blocks) {
+    const uint32_t nch = (uint32_t)p.D / 16u, per_row = nch * (uint32_t)p.H;
+    const uint32_t u = blockIdx.x * 256u + threadIdx.x;
+    if (u >= (uint32_t)p.T * per_row) return;  // the host keeps T * H * D / 16 below 2^31
+    const uint32_t i = u / per_row, rem = u - i * per_row;
+    const uint32_t h = rem / nch, c = rem - h * nch;
+    const uint4* src = (const uint4*)((const uint8_t*)p.k_new.base +
+                                      ((int64_t)i * p.k_new.stride[1] + (int64_t)h * p.k_new.stride[2] + c * 16) * EB);
+    uint4 raw[EB];
+#pragma unroll
+    for (int j = 0; j < EB; ++j) raw[j] = src[j];
     const int64_t sl = slot_at<XT, ST>(p, i);
-    if (sl < 0 || sl >= p.NB * 16) return;
-    const int64_t blk = sl >> 4;
-    const int off = (int)(sl & 15);
+#pragma unroll
+    for (int j = 0; j < EB; ++j) asm volatile("" ::"v"(raw[j].x), "v"(raw[j].y), "v"(raw[j].z), "v"(raw[j].w));
+    if (sl < 0 || sl >= cap) return;
     float f[16];
-    load16<XT>((const uint8_t*)p.k_new.base + (i * p.k_new.stride[1] + h * p.k_new.stride[2] + c * 16) * EB, f);
+    unpack16<XT>(raw, f);
     const Fp8Quant qk(p.k_scale[h * p.ks_s]);
-    *(uint4*)((uint8_t*)p.k_cache + blk * p.kc_s[0] + h * p.kc_s[2] + off * p.D + c * 16) = qk.pack16(f);
+    *(uint4*)((uint8_t*)p.k_cache + (sl >> 4) * p.kc_s[0] + (int64_t)h * p.kc_s[2] + (sl & 15) * p.D + c * 16) =
+        qk.pack16(f);
     return;
   }
-  const int64_t vb = (int64_t)blockIdx.x - k_blocks;
-  const int64_t g = vb / v_chunks;
-  const int hd = (int)(vb % v_chunks) * 256 + (int)threadIdx.x;
+  const uint32_t vb = blockIdx.x - k_blocks;
+  const uint32_t g = vb / v_chunks;
+  const int hd = (int)(vb - g * v_chunks) * 256 + (int)threadIdx.x;
   const bool mine = hd < p.H * p.D;
   const int h = mine ? hd / p.D : 0, d = mine ? hd % p.D : 0;
-  const Fp8Quant qv(p.v_scale[h * p.vs_s]);
-  const int64_t cap = p.NB * 16;
   // lane l holds the slot of row g * 16 - 1 + l (-1 outside [0, T)): the
-  // group's 16 rows, the row before and enough rows after for any run
+  // row before the group, the group's 16 rows and the 15 after them (a run
+  // starting in the group ends within 16 rows)
   const int lane = (int)(threadIdx.x & 63);
-  const int64_t r = g * 16 - 1 + lane;
+  const int64_t r = (int64_t)g * 16 - 1 + lane;
   const int64_t sl = r >= 0 && r < p.T ? slot_at<XT, ST>(p, r) : -1;
+  // rows g*16 .. g*16+30 of this thread's channel (clamped to the last row),
+  // loaded while the slots are in flight: a uniform row base + the thread's
+  // 32-bit (head, channel) offset (the host checks it fits)
+  const int last = (int)(p.T - 1 - (int64_t)g * 16 < 30 ? p.T - 1 - (int64_t)g * 16 : 30);
+  const uint8_t* gbase = (const uint8_t*)p.v_new.base + (int64_t)g * 16 * p.v_new.stride[1] * EB;
+  const uint32_t rs = (uint32_t)(p.v_new.stride[1] * EB);
+  const uint32_t voff = (uint32_t)(((int64_t)h * p.v_new.stride[2] + d) * EB);
+  T raw[31];
+#pragma unroll
+  for (int e = 0; e < 31; ++e) raw[e] = *(const T*)(gbase + (voff + (uint32_t)(e < last ? e : last) * rs));
   const bool valid = sl >= 0 && sl < cap;
   const int64_t up = __shfl_up(sl, 1, 64);
   // cont: this row takes the slot after the previous row's, in the same block
   const bool cont = valid && lane > 0 && sl == up + 1 && (sl & 15) != 0;
-  uint64_t starts = __ballot(valid && !cont && lane >= 1 && lane <= 16);
-  const uint64_t conts = __ballot(cont);
-  while (starts) {
-    const int st = __builtin_ctzll(starts);
-    starts &= starts - 1;
-    const int n = 1 + __builtin_ctzll(~(conts >> (st + 1)));  // run length (<= 16: runs stop at a block end)
-    const int64_t s0 = ((int64_t)__shfl(sl, st, 64));
-    const int64_t i = g * 16 - 1 + st;
-    if (!mine) continue;
-    uint8_t* vrow = (uint8_t*)p.v_cache + (s0 >> 4) * p.vc_s[0] + h * p.vc_s[2] + d * 16;
-    const typename XE::T* src =
-        (const typename XE::T*)p.v_new.base + i * p.v_new.stride[1] + (int64_t)h * p.v_new.stride[2] + d;
-    if (n == 16) {
-      float f[16];
+  const uint32_t vm = (uint32_t)__ballot(valid), cm = (uint32_t)__ballot(cont);
+  // Lane 1 + e <-> row e of the group.  Runs start at valid rows that do not
+  // continue the previous one; the group owns the valid rows 0..15 from its
+  // first run start on, and rows 16..30 that continue its last run.
+  const uint32_t starts = vm & ~cm & 0x1FFFEu;
+  if (!mine || starts == 0u) return;
+  const int e0 = __builtin_ctz(starts) - 1;     // first owned row, 0..15
+  const int ext = __builtin_ctz(~(cm >> 17));  // <= 15: runs stop at a block end
+  const uint32_t own = ((vm & 0x1FFFEu & ~((2u << e0) - 1u)) >> 1) | (((1u << ext) - 1u) << 16);
+  // each row's destination (block row base + token offset), per lane
+  const int64_t dst = valid ? (sl >> 4) * p.vc_s[0] + (sl & 15) : 0;
+  const uint32_t chan = (uint32_t)((int64_t)h * p.vc_s[2] + d * 16);
+  uint8_t* vcache = (uint8_t*)p.v_cache;
+  auto dst_of = [&](int e) {  // row e's destination (uniform)
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)(uint64_t)dst, e + 1);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)dst >> 32), e + 1);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
+  const Fp8Quant qv(p.v_scale[h * p.vs_s]);
+  const uint32_t ow = own >> e0;
+  if (ow <= 0xFFFFu) {
+    // the owned rows lie in e0 .. e0+15: one window of 16 values, quantized
+    // together
+    float win[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) f[e] = XE::load(src + e * p.v_new.stride[1]);
-      *(uint4*)vrow = qv.pack16(f);
-    } else {
-      const int o0 = (int)(s0 & 15);
-      for (int e = 0; e < n; ++e) vrow[o0 + e] = qv(XE::load(src + e * p.v_new.stride[1]));
+    for (int k = 0; k < 16; ++k) {
+      if (e0 == k) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) win[j] = XE::load(&raw[k + j]);
+      }
     }
+    const uint4 c4 = qv.pack16(win);
+    if (ow == 0xFFFFu && ((cm >> (e0 + 2)) & 0x7FFFu) == 0x7FFFu) {
+      // a run of 16 rows fills one block's channel row (its start is at
+      // token 0 of the block)
+      *(uint4*)(vcache + dst_of(e0) + chan) = c4;
+      return;
+    }
+    const uint32_t cw[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if ((ow >> j) & 1u) vcache[dst_of(e0 + j) + chan] = (uint8_t)(cw[j >> 2] >> (8 * (j & 3)));
+    return;
   }
+  // owned rows spread over more than 16 (a short run, then a run reaching
+  // past the group): byte by byte
+#pragma unroll
+  for (int e = 0; e < 31; ++e)
+    if ((own >> e) & 1u) vcache[dst_of(e) + chan] = qv(XE::load(&raw[e]));
 }
 
 // Whether kv_write_native_kernel applies: native cache layout with block
@@ -304,6 +353,12 @@ bool kv_write_native_ok(const KvWriteParams& p, int x_dt) {
     if (x->stride[3] != 1 || ((uintptr_t)x->base & 15)) return false;
     if (((x->stride[1] * eb) | (x->stride[2] * eb)) & 15) return false;
   }
+  // 32-bit index math and offsets: K pieces, a V row's (head, channel)
+  // offset plus 30 row strides, a V channel row's offset in a block
+  if (p.T * p.H * (p.D / 16) >= (int64_t)INT32_MAX) return false;
+  if (p.v_new.stride[1] < 0 || p.v_new.stride[2] < 0 || p.vc_s[2] < 0) return false;
+  if (((int64_t)(p.H - 1) * p.v_new.stride[2] + p.D + 30 * p.v_new.stride[1]) * eb >= (int64_t)UINT32_MAX) return false;
+  if ((int64_t)(p.H - 1) * p.vc_s[2] + (int64_t)p.D * 16 >= (int64_t)UINT32_MAX) return false;
   return true;
 }
 
@@ -825,8 +880,8 @@ int32_t launch_dequantize(const Rank4& q, const float* scales, int64_t s_stride,
 int32_t launch_kv_write_fp8(const KvWriteParams& p, int x_dt, int slot_dt, hipStream_t stream) {
   if (p.T == 0) return CF_OK;
   if (kv_write_native_ok(p, x_dt)) {
-    const int64_t k_blocks = ceil_div(p.T * p.H * (p.D / 16), 256);
-    const int v_chunks = (int)ceil_div((int64_t)p.H * p.D, 256);
+    const uint32_t k_blocks = (uint32_t)ceil_div(p.T * p.H * (p.D / 16), 256);
+    const uint32_t v_chunks = (uint32_t)ceil_div((int64_t)p.H * p.D, 256);
     const int64_t blocks = k_blocks + ceil_div(p.T, 16) * v_chunks;
     CF_CHECK(blocks < (int64_t)INT32_MAX, "kv_write: too many rows");
     const dim3 grid((unsigned)blocks);

@@ -231,11 +231,13 @@ def test_kv_write_bit_exact(gpu, layout, slot_dtype):
 
 @pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
 @pytest.mark.parametrize("h,d", [(8, 128), (3, 64)])
-def test_kv_write_runs_bit_exact(gpu, slot_dtype, h, d):
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_kv_write_runs_bit_exact(gpu, slot_dtype, h, d, x_dtype):
     """Slot patterns of a mixed step on the native layout: chunks starting
     mid-block (runs crossing the kernel's 16-row groups), whole blocks,
-    partial last blocks, single decode tokens, invalid slots inside a run,
-    and consecutive slots crossing a block boundary."""
+    partial last blocks, single decode tokens (a whole 16-row group of
+    them), invalid slots inside a run and past the cache's end, and
+    consecutive slots crossing a block boundary."""
     nb, bs = 64, 16
     gen = torch.Generator().manual_seed(5)
     slots: list[int] = []
@@ -245,12 +247,17 @@ def test_kv_write_runs_bit_exact(gpu, slot_dtype, h, d):
     slots += list(range(50 * bs + 2, 50 * bs + 13))  # partial run
     slots += [-1, 52 * bs + 1, 52 * bs + 2, -1, 52 * bs + 4]  # holes
     slots += list(range(60 * bs, 60 * bs + 16))  # one more whole block, unaligned to the row groups
+    lone = [9, 11, 13, 15, 17, 19, 22, 24, 26, 28, 30, 34, 36, 38, 42, 44, 46, 48, 54, 56]
+    slots += [b * bs + i for i, b in enumerate(lone)]  # decode tokens only, 20 blocks no other row uses
+    slots += [nb * bs - 3, nb * bs - 2, nb * bs - 1, nb * bs, nb * bs + 1, nb * bs + 40]  # the cache's end
+    inside = [x for x in slots if 0 <= x < nb * bs]
+    assert len(set(inside)) == len(inside)  # distinct slots: rows repeating a slot race
     t = len(slots)
     kc, vc = L.alloc_kv_cache(nb, bs, h, d, torch.float8_e4m3fn, gpu, "native")
     kc.view(torch.uint8).fill_(0xAA)
     vc.view(torch.uint8).fill_(0xAA)
-    k_new = torch.randn(t, h, d, generator=gen).to(torch.bfloat16).to(gpu)
-    v_new = torch.randn(t, h, d, generator=gen).to(torch.bfloat16).to(gpu)
+    k_new = torch.randn(t, h, d, generator=gen).to(x_dtype).to(gpu)
+    v_new = torch.randn(t, h, d, generator=gen).to(x_dtype).to(gpu)
     ks = ops.fp8_amax_scale(k_new)
     vs = ops.fp8_amax_scale(v_new)
     FP8KVCacheQuantizer.write_kv_fp8(k_new, v_new, torch.tensor(slots, dtype=slot_dtype, device=gpu), kc, vc, ks, vs)
@@ -260,7 +267,7 @@ def test_kv_write_runs_bit_exact(gpu, slot_dtype, h, d):
     wv = ofp8.quantize_per_head(v_new.float().cpu().numpy())[0]
     written = np.zeros((nb, bs), dtype=bool)
     for i, s in enumerate(slots):
-        if s < 0:
+        if s < 0 or s >= nb * bs:
             continue
         written[s // bs, s % bs] = True
         assert np.array_equal(kcodes[s // bs, s % bs], wk[i]), (i, s)
