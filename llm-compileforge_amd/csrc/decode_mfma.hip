@@ -714,15 +714,15 @@ __device__ __forceinline__ int64_t part_row(int2 d, int k) {
 
 // Combines the (m, l, o) partials of each (sequence b, KV head h) that the
 // decode kernel did not write whole: its own run's and its group's prefix
-// run's, each a record or the wave slots of a split run.  One wave per
-// (h, b); partial rows hold the G heads of h in consecutive rows.
-template <int QT, int D, int G>
+// run's, each a record or the wave slots of a split run.  NSL workgroups per
+// (h, b), each owning 1/NSL of the G x D output (more workgroups for small
+// grids); one wave of the first does the work when the partials fit its
+// registers, all four waves of each otherwise.  Partial rows hold the G
+// heads of h in consecutive rows.
+template <int QT, int D, int G, int NSL>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
   constexpr int E = G * D / 64;  // output elements per lane
   constexpr int kWaves = 4;
-  __shared__ float wgt[kWaves][64][G];
-  __shared__ float part_acc[kWaves - 1][E][64];
-  __shared__ float part_ml[kWaves - 1][2][G];
   const int h = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wave = uniform((int)threadIdx.x >> 6);
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
   if (nsrc == 0) return;  // written whole by the decode kernel (or empty)
   constexpr int KMAX = 64 / E;  // partials the register path holds
   if (nsrc <= KMAX) {
-    if (wave != 0) return;
+    if (wave != 0 || blockIdx.z != 0) return;
     // Few partials (the usual case): every load is issued at once -- each
     // lane's slice of every partial row and every (m, l) -- so the merge
     // costs one round trip after the descriptors.
@@ -795,124 +795,134 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
     }
     return;
   }
-  // Many partials (a sequence split over hundreds of waves): wave w takes
-  // partials w, w + 4, w + 8, ... in groups of 64, keeping its own running
-  // (max, sum, output) per query head; then wave 0 combines the four.
-  float acc[E];
+  // Many partials (a sequence split over hundreds of waves), in chunks of
+  // up to 256: the chunk's (m, l) pairs and row indices are staged in LDS;
+  // wave w reduces heads w, w + 4, ... (max, weights, weighted sum of l)
+  // and keeps their running (M, L); then each thread accumulates one
+  // 16-byte slice of the G x D output over every NP-th partial of the
+  // chunk, a batch of loads in flight at a time, and the NP phases are
+  // summed through LDS at the end.
+  constexpr int kChunk = 256;
+  constexpr int NF4 = G * D / 4 / NSL;            // 16-byte slices of the output in this workgroup
+  static_assert(G * D / 4 % NSL == 0, "output slices split evenly");
+  constexpr int FPT = NF4 > 256 ? NF4 / 256 : 1;  // slices per thread
+  constexpr int NP = NF4 >= 256 ? 1 : 256 / NF4;  // partial phases
+  constexpr int U = FPT == 1 ? 16 : 8;            // partials per batch of loads
+  __shared__ float sm[G][kChunk];                 // m, then the partial's weight
+  __shared__ float sl[G][kChunk];
+  __shared__ int srow[kChunk];
+  __shared__ float run_m[G], run_l[G], run_sc[G];
+  __shared__ float4 red[NP > 1 ? NP - 1 : 1][NP > 1 ? NF4 : 1];
+  const int tid = (int)threadIdx.x;
+  const int ph = FPT == 1 ? tid / NF4 : 0;
+  int fs[FPT], gs[FPT];
 #pragma unroll
-  for (int i = 0; i < E; ++i) acc[i] = 0.0f;
-  float Mg[G], Lg[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    Mg[g] = -INFINITY;
-    Lg[g] = 0.0f;
+  for (int j = 0; j < FPT; ++j) {
+    fs[j] = (int)blockIdx.z * NF4 + (FPT == 1 ? tid % NF4 : tid + 256 * j);
+    gs[j] = 4 * fs[j] / D;
   }
-  const int nloc = (nsrc - wave + kWaves - 1) / kWaves;  // this wave's partials
-  for (int j0 = 0; j0 < nloc; j0 += 64) {
-    const int kn = min(64, nloc - j0);
-    const int k = wave + kWaves * (j0 + lane);
-    const int64_t row = k < nown ? part_row(dn, k) : part_row(dp, k - nown);
-    float m[G], l[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m[g] = -INFINITY;
-      l[g] = 0.0f;
-      if (lane < kn) {
-        const float2 ml = *(const float2*)(p.ws_ml + (row + g) * 2);
-        m[g] = ml.x;
-        l[g] = ml.y;
-      }
-    }
-    float scale_old[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mnew = fmaxf(Mg[g], wave_max(m[g]));
-      scale_old[g] = (mnew == -INFINITY || Mg[g] == -INFINITY) ? (Mg[g] == -INFINITY ? 0.0f : 1.0f)
-                                                                 : __expf(Mg[g] - mnew);
-      const float wk = (m[g] == -INFINITY) ? 0.0f : __expf(m[g] - mnew);
-      Lg[g] = Lg[g] * scale_old[g] + wave_sum(l[g] * wk);
-      Mg[g] = mnew;
-      if (lane < kn) wgt[wave][lane][g] = wk;
-    }
-    // the weights pass between lanes of this wave only
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int i = 0; i < E; ++i) acc[i] *= scale_old[(lane + 64 * i) / D];
-    // U partial rows per step, all their loads issued before the sums
-    constexpr int U = E <= 8 ? 8 : (E <= 16 ? 4 : 2);
-    for (int kk = 0; kk < kn; kk += U) {
-      float ov[U][E];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int ks = wave + kWaves * (j0 + kk + u);
-        if (kk + u < kn) {
-          const int64_t rk = ks < nown ? part_row(dn, ks) : part_row(dp, ks - nown);
-          const float* o = p.ws_o + rk * D;
-#pragma unroll
-          for (int i = 0; i < E; ++i) ov[u][i] = o[lane + 64 * i];
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (kk + u < kn) {
-#pragma unroll
-          for (int i = 0; i < E; ++i) acc[i] += wgt[wave][kk + u][(lane + 64 * i) / D] * ov[u][i];
-        }
-      }
-    }
-    // the next group overwrites this wave's weights
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (tid < G) {
+    run_m[tid] = -INFINITY;
+    run_l[tid] = 0.0f;
   }
-  if (wave > 0) {
+  float4 acc[FPT];
 #pragma unroll
-    for (int i = 0; i < E; ++i) part_acc[wave - 1][i][lane] = acc[i];
-    if (lane == 0) {
+  for (int j = 0; j < FPT; ++j) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int c0 = 0; c0 < nsrc; c0 += kChunk) {
+    const int n = min(kChunk, nsrc - c0);
+    if (tid < n) {
+      const int k = c0 + tid;
+      const int row = (int)(k < nown ? part_row(dn, k) : part_row(dp, k - nown));
+      srow[tid] = row;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        part_ml[wave - 1][0][g] = Mg[g];
-        part_ml[wave - 1][1][g] = Lg[g];
+        const float2 ml = *(const float2*)(p.ws_ml + ((int64_t)row + g) * 2);
+        sm[g][tid] = ml.x;
+        sl[g][tid] = ml.y;
       }
     }
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  // combine: M = max of the waves' maxima, each wave's (L, acc) scaled to it
-  float sw[kWaves][G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float M = Mg[g];
-#pragma unroll
-    for (int w2 = 0; w2 < kWaves - 1; ++w2) M = fmaxf(M, part_ml[w2][0][g]);
-    sw[0][g] = Mg[g] == -INFINITY ? 0.0f : __expf(Mg[g] - M);
-    float L = Lg[g] * sw[0][g];
-#pragma unroll
-    for (int w2 = 0; w2 < kWaves - 1; ++w2) {
-      const float mw = part_ml[w2][0][g];
-      sw[w2 + 1][g] = mw == -INFINITY ? 0.0f : __expf(mw - M);
-      L += part_ml[w2][1][g] * sw[w2 + 1][g];
+    __syncthreads();
+    for (int g = wave; g < G; g += kWaves) {
+      float mx = -INFINITY;
+      for (int k = lane; k < n; k += 64) mx = fmaxf(mx, sm[g][k]);
+      mx = wave_max(mx);
+      const float mold = run_m[g];
+      const float mnew = fmaxf(mold, mx);
+      float ls = 0.0f;
+      for (int k = lane; k < n; k += 64) {
+        const float mk = sm[g][k];
+        const float w = mk == -INFINITY ? 0.0f : __expf(mk - mnew);
+        sm[g][k] = w;
+        ls += w * sl[g][k];
+      }
+      ls = wave_sum(ls);
+      if (lane == 0) {
+        const float sc = mold == -INFINITY ? 0.0f : __expf(mold - mnew);
+        run_sc[g] = sc;
+        run_l[g] = run_l[g] * sc + ls;
+        run_m[g] = mnew;
+      }
     }
-    Lg[g] = L;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FPT; ++j) {
+      const float sc = run_sc[gs[j]];
+      acc[j].x *= sc;
+      acc[j].y *= sc;
+      acc[j].z *= sc;
+      acc[j].w *= sc;
+    }
+    for (int kb = ph; kb < n; kb += NP * U) {
+      float4 ov[U][FPT];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = kb + u * NP;
+        if (k < n) {
+          const float4* o = (const float4*)(p.ws_o + (int64_t)srow[k] * D);
+#pragma unroll
+          for (int j = 0; j < FPT; ++j) ov[u][j] = o[fs[j]];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = kb + u * NP;
+        if (k < n) {
+#pragma unroll
+          for (int j = 0; j < FPT; ++j) {
+            const float w = sm[gs[j]][k];
+            acc[j].x += w * ov[u][j].x;
+            acc[j].y += w * ov[u][j].y;
+            acc[j].z += w * ov[u][j].z;
+            acc[j].w += w * ov[u][j].w;
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next chunk restages sm, sl, srow
+  }
+  if constexpr (NP > 1) {
+    if (ph > 0) red[ph - 1][fs[0] % NF4] = acc[0];
+    __syncthreads();
+    if (ph > 0) return;
+#pragma unroll
+    for (int q = 0; q < NP - 1; ++q) {
+      const float4 r = red[q][fs[0] % NF4];
+      acc[0].x += r.x;
+      acc[0].y += r.y;
+      acc[0].z += r.z;
+      acc[0].w += r.w;
+    }
   }
   uint16_t* out = (uint16_t*)p.out + (int64_t)b * p.o_sb;
 #pragma unroll
-  for (int i = 0; i < E; ++i) {
-    const int idx = lane + 64 * i;
-    const int g = idx / D, d = idx % D;
-    float a = 0.0f, lg = 0.0f;
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) {
-      if (gg == g) {
-        a = acc[i] * sw[0][gg];
-#pragma unroll
-        for (int w2 = 0; w2 < kWaves - 1; ++w2) a += part_acc[w2][i][lane] * sw[w2 + 1][gg];
-        lg = Lg[gg];
-      }
-    }
-    out[(int64_t)(h * G + g) * p.o_sh + d] = out_bits<QT>(lg > 0.0f ? a / lg : 0.0f);
+  for (int j = 0; j < FPT; ++j) {
+    const int g = gs[j], d = 4 * fs[j] % D;
+    const float lg = run_l[g];
+    auto nrm = [&](float a) { return out_bits<QT>(lg > 0.0f ? a / lg : 0.0f); };
+    uint2 packed;
+    packed.x = (uint32_t)nrm(acc[j].x) | ((uint32_t)nrm(acc[j].y) << 16);
+    packed.y = (uint32_t)nrm(acc[j].z) | ((uint32_t)nrm(acc[j].w) << 16);
+    *(uint2*)(out + (int64_t)(h * G + g) * p.o_sh + d) = packed;
   }
 }
 
@@ -934,6 +944,9 @@ int cu_count() {
 // (measured: 115.6 us vs 121.1 us vs 125.4 us for 1/2/3 per CU on the
 // Llama-3-8B shape).  The workspace holds slots for this many waves.
 constexpr int kStreamBlocksPerCU = 1;
+// Merge grids of fewer (sequence, KV head) pairs than this split each
+// output over 4 workgroups.
+constexpr int kMergeSplitBelow = 256;
 
 template <int KT, int D, bool PL, bool VTOK>
 constexpr size_t stream_lds_bytes() {
@@ -979,16 +992,23 @@ int32_t launch_t(const DecodeParams& p, hipStream_t stream) {
   int32_t rc;
   rc = v_token_major(p) ? launch_pl<QT, KT, D, true>(p, stream) : launch_pl<QT, KT, D, false>(p, stream);
   if (rc) return rc;
-  const dim3 grid(p.Hkv, p.B);
+  // Small grids (few sequences x KV heads) split each output over 4
+  // workgroups, so that long sequences' many partials are read by more CUs.
+  const bool split = (int64_t)p.B * p.Hkv < kMergeSplitBelow;
+  const dim3 grid(p.Hkv, p.B, split ? 4 : 1);
   ProfileScope prof("cf_decode_merge", stream);
+#define CF_MERGE(G)                                                                         \
+  if (split) CF_LAUNCH((decode_merge_kernel<QT, D, G, 4>), grid, dim3(256), 0, stream, p); \
+  else CF_LAUNCH((decode_merge_kernel<QT, D, G, 1>), grid, dim3(256), 0, stream, p);
   switch (p.G) {
-    case 1: CF_LAUNCH((decode_merge_kernel<QT, D, 1>), grid, dim3(256), 0, stream, p); break;
-    case 2: CF_LAUNCH((decode_merge_kernel<QT, D, 2>), grid, dim3(256), 0, stream, p); break;
-    case 4: CF_LAUNCH((decode_merge_kernel<QT, D, 4>), grid, dim3(256), 0, stream, p); break;
-    case 8: CF_LAUNCH((decode_merge_kernel<QT, D, 8>), grid, dim3(256), 0, stream, p); break;
-    case 16: CF_LAUNCH((decode_merge_kernel<QT, D, 16>), grid, dim3(256), 0, stream, p); break;
+    case 1: CF_MERGE(1) break;
+    case 2: CF_MERGE(2) break;
+    case 4: CF_MERGE(4) break;
+    case 8: CF_MERGE(8) break;
+    case 16: CF_MERGE(16) break;
     default: set_error("MFMA decode: unsupported GQA group %d", p.G); return CF_ERR_UNSUPPORTED;
   }
+#undef CF_MERGE
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
 }

@@ -252,12 +252,15 @@ def test_hal_backend_paged_attention(gpu):
 
 
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
-def test_long_single_sequence_split_over_many_waves(gpu, kv_dtype):
-    """One 30000-token sequence: every KV head's run is split over hundreds of
-    waves, so the merge combines more than 64 partials per head."""
-    print(f"[case] long single sequence kv={kv_dtype}", flush=True)
+@pytest.mark.parametrize("n,hq,hkv,d", [(30000, 32, 8, 128), (40000, 32, 2, 128), (20000, 4, 4, 64),
+                                        (25000, 16, 2, 64), (3000, 8, 1, 64)])
+def test_long_single_sequence_split_over_many_waves(gpu, kv_dtype, n, hq, hkv, d):
+    """One long sequence: every KV head's run is split over hundreds of
+    waves, so the merge combines more than its register path holds -- up to
+    ~1,000 partials per head (several 256-partial chunks) with one KV head
+    or two, G from 1 to 16 (one to two 16-byte output slices per thread)."""
+    print(f"[case] long single sequence kv={kv_dtype} n={n} hq={hq} hkv={hkv} d={d}", flush=True)
     g = torch.Generator(device=gpu).manual_seed(12)
-    n, hq, hkv, d = 30000, 32, 8, 128
     nb = (n + 15) // 16 + 3
     perm = torch.randperm(nb, generator=torch.Generator().manual_seed(3)).tolist()
     q = torch.randn(1, hq, d, generator=g, device=gpu).to(torch.bfloat16)
