@@ -89,12 +89,17 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
     const typename KE::T* krow =
         kbase + (blk_ok ? blk : 0) * p.k_s[0] + (int64_t)(tok % bs) * p.k_s[1] + (int64_t)h * p.k_s[2];
     for (int d0 = 0; d0 < D; d0 += 16 * kChunk) {
+      // every load issued before any is used: out-of-range channels read
+      // channel 0 of the row (or of block 0) and are zeroed afterwards
       float kv[kChunk];
 #pragma unroll
       for (int c = 0; c < kChunk; ++c) {
         const int d = d0 + sub + 16 * c;
-        kv[c] = (blk_ok && d < D) ? KE::load(krow + (int64_t)d * p.k_s[3]) : 0.0f;
+        kv[c] = KE::load(krow + (int64_t)(d < D ? d : 0) * p.k_s[3]);
       }
+#pragma unroll
+      for (int c = 0; c < kChunk; ++c)
+        if (!blk_ok || d0 + sub + 16 * c >= D) kv[c] = 0.0f;
       for (int g = 0; g < G; ++g) {
         const float* qg = sq + g * D;
         float acc = 0.0f;
@@ -151,13 +156,24 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
     const int g = active ? o / D : 0, d = active ? o % D : 0;
     float acc = 0.0f;
     if (active) {
-      for (int t = grp; t < count; t += ng) {
-        const int tok = start + t;
-        const int64_t blk = sblk[t / bs];
-        if ((uint64_t)blk >= (uint64_t)p.NB) continue;
-        const typename KE::T* vrow =
-            vbase + blk * p.v_s[0] + (int64_t)(tok % bs) * p.v_s[1] + (int64_t)h * p.v_s[2];
-        acc = fmaf(sc[g * PT + t], KE::load(vrow + (int64_t)d * p.v_s[3]), acc);
+      // kU tokens per step, their loads issued together (an invalid block
+      // reads block 0 and gets weight 0)
+      constexpr int kU = 8;
+      for (int t0 = grp; t0 < count; t0 += kU * ng) {
+        float vv[kU], ww[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          const int t = t0 + u * ng;
+          const int tt = t < count ? t : grp;
+          const int64_t blk = sblk[tt / bs];
+          const bool ok = t < count && (uint64_t)blk < (uint64_t)p.NB;
+          const typename KE::T* vrow = vbase + (ok ? blk : 0) * p.v_s[0] + (int64_t)((start + tt) % bs) * p.v_s[1] +
+                                       (int64_t)h * p.v_s[2];
+          vv[u] = KE::load(vrow + (int64_t)d * p.v_s[3]);
+          ww[u] = ok ? sc[g * PT + tt] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) acc = fmaf(ww[u], vv[u], acc);
       }
     }
     if (ng > 1) {
