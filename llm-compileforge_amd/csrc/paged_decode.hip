@@ -90,12 +90,15 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
         kbase + (blk_ok ? blk : 0) * p.k_s[0] + (int64_t)(tok % bs) * p.k_s[1] + (int64_t)h * p.k_s[2];
     for (int d0 = 0; d0 < D; d0 += 16 * kChunk) {
       // every load issued before any is used: out-of-range channels read
-      // channel 0 of the row (or of block 0) and are zeroed afterwards
+      // channel 0 of the row (or of block 0) and are zeroed afterwards; a
+      // cache without blocks (possibly a null pointer) is not read at all
       float kv[kChunk];
+      if (p.NB > 0) {
 #pragma unroll
-      for (int c = 0; c < kChunk; ++c) {
-        const int d = d0 + sub + 16 * c;
-        kv[c] = KE::load(krow + (int64_t)(d < D ? d : 0) * p.k_s[3]);
+        for (int c = 0; c < kChunk; ++c) {
+          const int d = d0 + sub + 16 * c;
+          kv[c] = KE::load(krow + (int64_t)(d < D ? d : 0) * p.k_s[3]);
+        }
       }
 #pragma unroll
       for (int c = 0; c < kChunk; ++c)
@@ -157,9 +160,9 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
     float acc = 0.0f;
     if (active) {
       // kU tokens per step, their loads issued together (an invalid block
-      // reads block 0 and gets weight 0)
+      // reads block 0 and gets weight 0; a cache without blocks is not read)
       constexpr int kU = 8;
-      for (int t0 = grp; t0 < count; t0 += kU * ng) {
+      for (int t0 = grp; p.NB > 0 && t0 < count; t0 += kU * ng) {
         float vv[kU], ww[kU];
 #pragma unroll
         for (int u = 0; u < kU; ++u) {

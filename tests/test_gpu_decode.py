@@ -143,6 +143,22 @@ def test_edge_lengths(gpu):
     assert_close(out[1:], ref[1:], case.q.dtype, "edge lengths")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_cache_without_blocks(gpu, dtype):
+    """A cache of zero blocks (its data pointer may be NULL): every table
+    entry is outside the pool, so every output is zero and the cache is
+    never read."""
+    print(f"[case] empty cache {dtype}", flush=True)
+    q = torch.randn(2, 4, 64, device=gpu).to(dtype)
+    kc = torch.empty(0, 16, 2, 64, dtype=dtype, device=gpu)
+    vc = torch.empty(0, 16, 2, 64, dtype=dtype, device=gpu)
+    tables = torch.tensor([[0, 1], [5, 2]], dtype=torch.int32, device=gpu)
+    lens = torch.tensor([20, 3], dtype=torch.int32, device=gpu)
+    out = paged_attention_tensors(q, kc, vc, tables, lens, 16, 0.125)
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and torch.count_nonzero(out).item() == 0
+
+
 def test_dict_api_matches_tensor_api_and_reference_rules(gpu):
     case = workloads.make_case("c2_tinyllama", device=gpu, seed=5, batch=6)
     kc, vc, ks, vs = workloads.materialize(case, "native")
