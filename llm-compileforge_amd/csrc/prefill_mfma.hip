@@ -350,6 +350,10 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
   const int li = lane & 15, lq = lane >> 4;
   const int n_items = header[0];
   const int cap = p.Mb * 16;
+  // Beside the memory-bound decode kernel (a mixed step's two streams), a
+  // SIMD holds one wave of each; the prefill's, on the step's critical path,
+  // issues first.  Among the prefill's own waves the priorities are equal.
+  __builtin_amdgcn_s_setprio(2);
 
   for (;;) {
     if (tid == 0) s_item = atomicAdd(&header[1], 1);
