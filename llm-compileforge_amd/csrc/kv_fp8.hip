@@ -131,38 +131,6 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteParams p) {
   }
 }
 
-// 16 consecutive source elements (16-byte aligned) as floats.
-template <int XT>
-__device__ __forceinline__ void load16(const void* src, float* f) {
-  const uint4* s = (const uint4*)src;
-  if constexpr (XT == kF32) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 u = s[i];
-      f[4 * i] = u2f(u.x);
-      f[4 * i + 1] = u2f(u.y);
-      f[4 * i + 2] = u2f(u.z);
-      f[4 * i + 3] = u2f(u.w);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint4 u = s[i];
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if constexpr (XT == kBF16) {
-          f[8 * i + 2 * j] = f32_from_bf16_bits(w[j] & 0xFFFFu);
-          f[8 * i + 2 * j + 1] = f32_from_bf16_bits(w[j] >> 16);
-        } else {
-          f[8 * i + 2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xFFFFu));
-          f[8 * i + 2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
-        }
-      }
-    }
-  }
-}
-
 // Streaming (non-temporal) 16-byte accesses for data touched once.
 typedef unsigned nt_u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 stream_load16(const void* p) {

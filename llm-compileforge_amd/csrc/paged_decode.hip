@@ -25,43 +25,6 @@ namespace {
 
 constexpr int kGenericThreads = 256;
 
-// 16 consecutive elements of type KT (16-byte aligned) as floats.
-template <int KT>
-__device__ __forceinline__ void load16f(const void* src, float* f) {
-  const uint4* s = (const uint4*)src;
-  if constexpr (KT == kF32) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 u = s[i];
-      f[4 * i] = u2f(u.x);
-      f[4 * i + 1] = u2f(u.y);
-      f[4 * i + 2] = u2f(u.z);
-      f[4 * i + 3] = u2f(u.w);
-    }
-  } else if constexpr (KT == kE4M3) {
-    const uint4 u = s[0];
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int j = 0; j < 16; ++j) f[j] = f32_from_e4m3((w[j >> 2] >> (8 * (j & 3))) & 0xFFu);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint4 u = s[i];
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if constexpr (KT == kBF16) {
-          f[8 * i + 2 * j] = f32_from_bf16_bits(w[j] & 0xFFFFu);
-          f[8 * i + 2 * j + 1] = f32_from_bf16_bits(w[j] >> 16);
-        } else {
-          f[8 * i + 2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xFFFFu));
-          f[8 * i + 2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
-        }
-      }
-    }
-  }
-}
-
 __device__ __forceinline__ int effective_len(const DecodeParams& p, int b) {
   int ctx = p.seq_lens[(int64_t)b * p.sl_s];
   const int cap = p.Mb * p.bs;
@@ -206,7 +169,7 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
         const int64_t blk = sblk[bi];
         if ((uint64_t)blk >= (uint64_t)p.NB) continue;
         float v16[16];
-        load16f<KT>(vbase + blk * p.v_s[0] + (int64_t)h * p.v_s[2] + (int64_t)d * p.v_s[3], v16);
+        load16<KT>(vbase + blk * p.v_s[0] + (int64_t)h * p.v_s[2] + (int64_t)d * p.v_s[3], v16);
         const int t0 = bi * 16;
 #pragma unroll
         for (int e = 0; e < 16; ++e)
