@@ -580,8 +580,16 @@ def main() -> None:
     assert main_n == args.steps, f"expected {args.steps} {kernel_name} launches, timed {main_n}"
     log(f"{ms_step * 1e3:.1f} us/step ({ms_step_stamped * 1e3:.1f} with stamped launches); decode kernel "
         f"{main_ms / main_n * 1e3:.1f} us, merge {red_ms / max(red_n, 1) * 1e3:.1f} us")
-    # One kernel of a step cannot outlast the step.
-    assert main_ms / main_n <= ms_step, (main_ms / main_n, ms_step)
+    # One kernel of a step cannot outlast the step.  Under rocprofv3 (which
+    # sets ROCPROF_* in the program's environment) every stamped launch is
+    # intercepted and slowed, so short kernels can read longer than the
+    # unprofiled step; the line then records that instead of failing.
+    over = main_ms / main_n > ms_step
+    profiled = any(k.startswith("ROCPROF_") for k in os.environ)
+    assert not over or profiled, (main_ms / main_n, ms_step)
+    if over:
+        log(f"note: under the profiler the stamped {kernel_name} launch ({main_ms / main_n * 1e3:.1f} us) reads "
+            f"longer than the step ({ms_step * 1e3:.1f} us)")
 
     avg_main_s = main_ms / max(main_n, 1) / 1e3
     achieved = ab["unique"] / avg_main_s / 1e9
