@@ -192,8 +192,9 @@ int32_t cf_prefill_chunk_workspace_bytes(int64_t num_q_tokens, int64_t num_chunk
  * (cf_kv_write_fp8).
  *
  *   q            [Tq, Hq, D]           bf16, D stride 1, rows of all chunks
- *   k_cache,     [NB, 16, Hkv, D]      bf16 | e4m3fn, native layout (as the
- *   v_cache                            MFMA decode path)
+ *   k_cache,     [NB, 16, Hkv, D]      bf16 | e4m3fn, native or paired tiles,
+ *   v_cache                            or the reference's token-major rows
+ *                                      (16-byte aligned token rows)
  *   block_tables [N, Mb]               i32, one row per chunk's sequence
  *   seq_lens     [N]                   i32, tokens of the sequence including
  *                                      the chunk

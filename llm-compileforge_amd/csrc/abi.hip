@@ -551,8 +551,8 @@ int32_t cf_prefill_chunk_fp8(const CfTensor* q, const CfTensor* k_cache, const C
     CF_CHECK(k_scale == nullptr && v_scale == nullptr, "k_scale/v_scale apply to f8e4m3fn caches only");
   }
   if (!prefill_supported(p, vq.dtype, vk.dtype)) {
-    set_error("prefill: needs head_dim 64/128, GQA group 1/2/4/8/16, native-layout caches with 16-byte "
-              "aligned blocks and heads, and 16-byte aligned q rows");
+    set_error("prefill: needs head_dim 64/128, GQA group 1/2/4/8/16, native or token-major caches with "
+              "16-byte aligned blocks, heads and token rows, and 16-byte aligned q rows");
     return CF_ERR_UNSUPPORTED;
   }
   if (Tq == 0 || N == 0) return CF_OK;

@@ -166,6 +166,14 @@ struct Geo {
   static constexpr int VU = 2 * D * VPER;       // V loads per tile
   static constexpr int KPT = (KU + 255) / 256;  // per thread
   static constexpr int VPT = (VU + 255) / 256;
+  // Token-major V (the reference's [NB, bs, Hkv, D] layout): a 16-byte load
+  // is VCH channels of one token; the tile is staged as 32 rows of 16-bit
+  // values, RS bytes apart (16 bytes of padding: no bank conflicts), and
+  // read back transposed into the operand order.
+  static constexpr int VCH = 16 / KB;                  // channels per load
+  static constexpr int VCPR = D / VCH;                 // loads per token row
+  static constexpr int VRS = vtok_row_stride<D, 2>();  // LDS bytes per staged row
+  static constexpr int VENT_TOK = (32 * VRS + 15) / 16;
 };
 
 struct TileIds {
@@ -219,8 +227,11 @@ __device__ __forceinline__ KPiece k_piece(int u) {
   return q;
 }
 
-// Global loads of one K/V tile into registers (16 bytes each).
-template <int KT, int D>
+// Global loads of one K/V tile into registers (16 bytes each).  K rows are
+// token rows of k_s[1] elements' stride (head_dim in the native layout);
+// V is the native tile (VTOK false: channel rows of 16 tokens) or
+// token-major (a load is one token's VCH channels).
+template <int KT, int D, bool VTOK>
 __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillParams& p, const TileIds& t, int h,
                                            int tid) {
   using Gm = Geo<KT, D>;
@@ -233,7 +244,7 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
       const KPiece q = k_piece<KT, D>(u);
       const int blk = uniform(q.X) ? t.b : t.a;
       const uint8_t* b = kbase + ((int64_t)blk * p.k_s[0] + (int64_t)h * p.k_s[2]) * Gm::KB;
-      const uint32_t off = (uint32_t)((q.row * D + q.lq * (D / 4)) * Gm::KB + q.cp * 16);
+      const uint32_t off = (uint32_t)((q.row * p.k_s[1] + q.lq * (D / 4)) * Gm::KB + q.cp * 16);
       kr[i] = *(const uint4*)(b + off);
     }
   }
@@ -241,15 +252,32 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
   for (int i = 0; i < Gm::VPT; ++i) {
     const int u = tid + 256 * i;
     if (Gm::VU % 256 == 0 || u < Gm::VU) {
-      // 16 bytes of channel d of block X: all 16 tokens (e4m3) or half of them (bf16)
-      const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
-      const int d = rem / Gm::VPER, part = rem % Gm::VPER;
-      const int blk = uniform(X) ? t.b : t.a;
-      const uint8_t* b = vbase + ((int64_t)blk * p.v_s[0] + (int64_t)h * p.v_s[2]) * Gm::KB;
-      const uint32_t off = (uint32_t)(d * 16 * Gm::KB + part * 16);
-      vr[i] = *(const uint4*)(b + off);
+      if constexpr (VTOK) {
+        // 16 bytes of token r of block X: channels VCH c .. VCH c + VCH - 1
+        const int X = u / (16 * Gm::VCPR), r = (u / Gm::VCPR) % 16, c = u % Gm::VCPR;
+        const int blk = uniform(X) ? t.b : t.a;
+        const uint8_t* b = vbase + ((int64_t)blk * p.v_s[0] + (int64_t)h * p.v_s[2]) * Gm::KB;
+        const uint32_t off = (uint32_t)(r * p.v_s[1] * Gm::KB + c * 16);
+        vr[i] = *(const uint4*)(b + off);
+      } else {
+        // 16 bytes of channel d of block X: all 16 tokens (e4m3) or half of them (bf16)
+        const int X = u / (D * Gm::VPER), rem = u % (D * Gm::VPER);
+        const int d = rem / Gm::VPER, part = rem % Gm::VPER;
+        const int blk = uniform(X) ? t.b : t.a;
+        const uint8_t* b = vbase + ((int64_t)blk * p.v_s[0] + (int64_t)h * p.v_s[2]) * Gm::KB;
+        const uint32_t off = (uint32_t)(d * 16 * Gm::KB + part * 16);
+        vr[i] = *(const uint4*)(b + off);
+      }
     }
   }
+}
+
+// All ones when token r of block X (of a tile whose blocks' validity bits
+// are `ok`) is below `valid`, tile-relative, and its block is valid; else 0.
+__device__ __forceinline__ uint32_t vtok_keep_mask(int ok, int X, int r, int valid) {
+  const uint32_t blk_ok = (uint32_t)(ok >> X) & 1u;
+  const uint32_t in_len = (uint32_t)(16 * X + r < valid);
+  return 0u - (blk_ok & in_len);
 }
 
 // Converts the staged registers and writes them in operand order: K entry
@@ -258,7 +286,7 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
 // V tokens at or past `valid` (tile-relative) or in an invalid block become
 // zero (cache slots there may hold any bits, NaN codes included).
 // FULL: the caller knows every token of the tile is valid.
-template <int KT, int D, bool FULL = false>
+template <int KT, int D, bool VTOK, bool FULL = false>
 __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const uint4* vr, const TileIds& t,
                                             int valid, int tid) {
   using Gm = Geo<KT, D>;
@@ -280,6 +308,31 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
   // Tiles whose 32 tokens are all valid (all but an item's last tile) skip
   // the masking (a wave-uniform branch).
   const bool full = FULL || (valid >= 32 && t.ok == 3);
+  if constexpr (VTOK) {
+    // token row 16 X + r of the staged tile, 16-bit; a token past `valid`
+    // or in an invalid block is written as zeros.  The keep mask is formed
+    // arithmetically: written as a short-circuit select, the ROCm 7.2
+    // compiler dropped the keep lanes' copy of the loaded value (bf16,
+    // head_dim 64) and wrote zeros.
+    uint8_t* rows = (uint8_t*)vl;
+#pragma unroll
+    for (int i = 0; i < Gm::VPT; ++i) {
+      const int u = tid + 256 * i;
+      if (Gm::VU % 256 == 0 || u < Gm::VU) {
+        const int X = u / (16 * Gm::VCPR), r = (u / Gm::VCPR) % 16, c = u % Gm::VCPR;
+        const uint32_t km = full ? ~0u : vtok_keep_mask(t.ok, X, r, valid);
+        const uint4 v = make_uint4(vr[i].x & km, vr[i].y & km, vr[i].z & km, vr[i].w & km);
+        uint8_t* row = rows + (16 * X + r) * Gm::VRS;
+        if constexpr (KT == kE4M3) {
+          *(uint4*)(row + 32 * c) = __builtin_bit_cast(uint4, e4m3x8_to_f16(v.x, v.y));
+          *(uint4*)(row + 32 * c + 16) = __builtin_bit_cast(uint4, e4m3x8_to_f16(v.z, v.w));
+        } else {
+          *(uint4*)(row + 16 * c) = v;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < Gm::VPT; ++i) {
     const int u = tid + 256 * i;
@@ -312,9 +365,21 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
 // Zeroes, in the staged registers, the V tokens at or past `valid`
 // (tile-relative) or in an invalid block, so that the tile can then be
 // written without masking.
-template <int KT, int D>
+template <int KT, int D, bool VTOK>
 __device__ __forceinline__ void mask_staged_v(uint4* vr, const TileIds& t, int valid, int tid) {
   using Gm = Geo<KT, D>;
+  if constexpr (VTOK) {
+#pragma unroll
+    for (int i = 0; i < Gm::VPT; ++i) {
+      const int u = tid + 256 * i;
+      if (Gm::VU % 256 == 0 || u < Gm::VU) {
+        const int X = u / (16 * Gm::VCPR), r = (u / Gm::VCPR) % 16;
+        const uint32_t km = vtok_keep_mask(t.ok, X, r, valid);
+        vr[i] = make_uint4(vr[i].x & km, vr[i].y & km, vr[i].z & km, vr[i].w & km);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < Gm::VPT; ++i) {
     const int u = tid + 256 * i;
@@ -334,7 +399,7 @@ __device__ __forceinline__ void mask_staged_v(uint4* vr, const TileIds& t, int v
   }
 }
 
-template <int KT, int D, int G>
+template <int KT, int D, int G, bool VTOK>
 __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, const int32_t* __restrict__ tables,
                                                               const int4* __restrict__ items,
                                                               const int4* __restrict__ chunks, int* header,
@@ -343,7 +408,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
   using Gm = Geo<KT, D>;
   constexpr int NC = Gm::NC, NV = Gm::NV;
   constexpr int RB = kCols / G;
-  __shared__ uint4 lds[2][Gm::KENT + Gm::VENT];
+  __shared__ uint4 lds[2][Gm::KENT + (VTOK ? Gm::VENT_TOK : Gm::VENT)];
   __shared__ int s_item;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uniform(tid >> 6);
@@ -438,10 +503,10 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     TileIds id1 = nt > 1 ? tile_ids(p, trow, 1, kvlen) : id0;
     TileIds id2 = nt > 2 ? tile_ids(p, trow, 2, kvlen) : id1;
     if (nt > 0) {
-      stage_load<KT, D>(kr, vr, p, id0, h, tid);
-      stage_write<KT, D>(lds[0], kr, vr, id0, kvlen, tid);
+      stage_load<KT, D, VTOK>(kr, vr, p, id0, h, tid);
+      stage_write<KT, D, VTOK>(lds[0], kr, vr, id0, kvlen, tid);
     }
-    if (nt > 1) stage_load<KT, D>(kr, vr, p, id1, h, tid);
+    if (nt > 1) stage_load<KT, D, VTOK>(kr, vr, p, id1, h, tid);
     __syncthreads();
 
     using POp = typename std::conditional<KT == kE4M3, f16x8_t, bf16x8_t>::type;
@@ -557,7 +622,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     auto step = [&](auto par, int j) {
       constexpr int P = decltype(par)::value;
       const int valid_next = kvlen - 32 * (j + 1);
-      if (!(j + 2 <= nfull && id1.ok == 3)) mask_staged_v<KT, D>(vr, id1, valid_next, tid);
+      if (!(j + 2 <= nfull && id1.ok == 3)) mask_staged_v<KT, D, VTOK>(vr, id1, valid_next, tid);
       // table entries of tile j + 3, read now and resolved after the math
       int raw_a = -1, raw_b = -1;
       if (j + 3 < nt) {
@@ -582,8 +647,8 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       POp pa, pla, pb, plb;
       // QK^T of column tile 0 beside the next tile's conversion into LDS
       qk(K0, a1, a2, s1a, s2a);
-      stage_write<KT, D, true>(lds[1 - P], kr, vr, id1, valid_next, tid);
-      stage_load<KT, D>(kr, vr, p, id2, h, tid);
+      stage_write<KT, D, VTOK, true>(lds[1 - P], kr, vr, id1, valid_next, tid);
+      stage_load<KT, D, VTOK>(kr, vr, p, id2, h, tid);
       __builtin_amdgcn_sched_group_barrier(0x100, 2 * NC, 0);
 #pragma unroll
       for (int i = 0; i < kQkMfma; ++i) {
@@ -598,7 +663,8 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       // across the QK^T products)
       qk(K1, a1, a2, s1b, s2b);
 #pragma unroll
-      for (int t = 0; t < NV; ++t) vraw[t] = vl[t * 64 + lane];
+      for (int t = 0; t < NV; ++t)
+        vraw[t] = VTOK ? vtok_operand16<D>((const uint8_t*)vl, t, li, lq) : vl[t * 64 + lane];
       const float mta = lane_max(s1a, s2a);
       // keeps the max here, beside the MFMAs, instead of sunk past the
       // next branch to its use
@@ -606,7 +672,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
 #pragma unroll
       for (int i = 0; i < kQkMfma; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(0x100, NV / kQkMfma > 0 ? NV / kQkMfma : 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, (VTOK ? 2 : 1) * NV / kQkMfma > 0 ? (VTOK ? 2 : 1) * NV / kQkMfma : 1, 1);
         __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);
       }
       if (edge) mask(K1, s1b, s2b, id0.ok, tok0);
@@ -672,12 +738,12 @@ int prefill_cus() {
 
 constexpr int kItemBlocksPerCU = 2;  // resident workgroups per CU (8 waves)
 
-template <int KT, int D, int G>
+template <int KT, int D, int G, bool VTOK>
 int32_t launch_t(PrefillParams& p, hipStream_t stream) {
   static int per_cu = 0;
   if (per_cu == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_item_kernel<KT, D, G>, 256, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_item_kernel<KT, D, G, VTOK>, 256, 0) != hipSuccess ||
         n < 1)
       n = 1;
     per_cu = n < kItemBlocksPerCU ? n : kItemBlocksPerCU;
@@ -689,24 +755,30 @@ int32_t launch_t(PrefillParams& p, hipStream_t stream) {
   CF_HIP_CHECK(hipGetLastError());
   {
     ProfileScope prof("cf_prefill_mfma", stream);
-    CF_LAUNCH((prefill_item_kernel<KT, D, G>), dim3(prefill_cus() * per_cu), dim3(256), 0, stream, p,
+    CF_LAUNCH((prefill_item_kernel<KT, D, G, VTOK>), dim3(prefill_cus() * per_cu), dim3(256), 0, stream, p,
                        p.tables, (const int4*)p.items, (const int4*)p.chunks, p.header, p.k_scale, p.v_scale);
   }
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
 }
 
-template <int KT, int D>
-int32_t launch_g(PrefillParams& p, hipStream_t stream) {
+template <int KT, int D, bool VTOK>
+int32_t launch_v(PrefillParams& p, hipStream_t stream) {
   switch (p.G) {
-    case 1: return launch_t<KT, D, 1>(p, stream);
-    case 2: return launch_t<KT, D, 2>(p, stream);
-    case 4: return launch_t<KT, D, 4>(p, stream);
-    case 8: return launch_t<KT, D, 8>(p, stream);
-    case 16: return launch_t<KT, D, 16>(p, stream);
+    case 1: return launch_t<KT, D, 1, VTOK>(p, stream);
+    case 2: return launch_t<KT, D, 2, VTOK>(p, stream);
+    case 4: return launch_t<KT, D, 4, VTOK>(p, stream);
+    case 8: return launch_t<KT, D, 8, VTOK>(p, stream);
+    case 16: return launch_t<KT, D, 16, VTOK>(p, stream);
   }
   set_error("prefill: unsupported GQA group %d", p.G);
   return CF_ERR_UNSUPPORTED;
+}
+
+// V in token rows (token stride != 1) or the native channel rows
+template <int KT, int D>
+int32_t launch_g(PrefillParams& p, hipStream_t stream) {
+  return p.v_s[1] != 1 ? launch_v<KT, D, true>(p, stream) : launch_v<KT, D, false>(p, stream);
 }
 
 uint64_t pad256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
@@ -720,7 +792,12 @@ bool prefill_supported(const PrefillParams& p, int q_dt, int kv_dt) {
   if (p.G != 1 && p.G != 2 && p.G != 4 && p.G != 8 && p.G != 16) return false;
   if (p.NB < 1) return false;
   const int kb = kv_dt == kE4M3 ? 1 : 2;
-  if (p.k_s[3] != 1 || p.k_s[1] != p.D || p.v_s[1] != 1 || p.v_s[3] != 16) return false;
+  // native (K token rows of head_dim, V channel rows of 16 tokens) or
+  // token-major (the reference's layout: both caches in token rows)
+  const bool native = p.k_s[3] == 1 && p.k_s[1] == p.D && p.v_s[1] == 1 && p.v_s[3] == 16;
+  const bool token_major = p.k_s[3] == 1 && p.v_s[3] == 1 && p.v_s[1] != 1 && (p.k_s[1] * kb) % 16 == 0 &&
+                           (p.v_s[1] * kb) % 16 == 0;
+  if (!native && !token_major) return false;
   if ((p.k_s[0] * kb) % 16 || (p.k_s[2] * kb) % 16 || (p.v_s[0] * kb) % 16 || (p.v_s[2] * kb) % 16) return false;
   if (((uintptr_t)p.k & 15) || ((uintptr_t)p.v & 15)) return false;
   if (((uintptr_t)p.q & 15) || (p.q_sr * 2) % 16 || (p.q_sh * 2) % 16) return false;

@@ -290,8 +290,9 @@ def chunked_prefill_attention(
     Args:
         q: [Tq, Hq, D] bf16, the query rows of all chunks.
         k_cache, v_cache: [num_blocks, 16, Hkv, D] bf16 or float8_e4m3fn in
-            the native layout (cf_hip.layout.alloc_kv_cache); the chunk's
-            own K/V must already be written.
+            any layout of cf_hip.layout.alloc_kv_cache (the reference's
+            token-major one included); the chunk's own K/V must already be
+            written.
         block_tables: int32 [N, Mb], one row per chunk's sequence.
         seq_lens: int32 [N], tokens of each sequence including its chunk.
         q_start: int32 [N + 1]; chunk n owns q rows [q_start[n], q_start[n+1]).

@@ -77,7 +77,7 @@ def _prefill(case, t, **kw):
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 1, 128), (32, 2, 64), (4, 2, 128),
                                       (16, 8, 64)])
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
-@pytest.mark.parametrize("layout", ["paired", "native"])
+@pytest.mark.parametrize("layout", ["paired", "native", "token_major"])
 def test_shapes_match_oracle(gpu, hq, hkv, d, kv_dtype, layout):
     print(f"[case] prefill hq={hq} hkv={hkv} d={d} kv={kv_dtype} layout={layout}", flush=True)
     case = workloads.make_mixed_case(device=gpu, seed=hq + d, chunks=[1, 17, 64, 100, 33],
@@ -103,12 +103,14 @@ def test_chunk_mixes(gpu, chunks, cached):
     assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, "chunk mix")
 
 
-def test_edge_rules(gpu):
+@pytest.mark.parametrize("layout", ["paired", "token_major"])
+def test_edge_rules(gpu, layout):
     """Overlapping and empty chunks, rows outside every chunk (left as they
     were), rows at negative positions (zeros), lengths past the table."""
+    print(f"[case] prefill edge rules layout={layout}", flush=True)
     case = workloads.make_mixed_case(device=gpu, seed=9, chunks=[40, 30, 20], cached=[10, 50, 0],
                                      decode_lens=[])
-    t = workloads.materialize_mixed(case)
+    t = workloads.materialize_mixed(case, layout)
     _write_new_rows(case, t)
     q_start = [3, 45, 41, 41, 80]  # chunk 1 overlaps chunk 0; chunk 2 is empty after the cut
     lens = [52, 20, 20, 5]  # chunk 3: 35 rows, 5 tokens -> 30 rows at negative positions
@@ -133,6 +135,30 @@ def test_edge_rules(gpu):
     ref2, _ = oracle_prefill(case, t, q=case.q_prefill[:8], tables=case.prefill_tables[:1], lens=[cap + 100],
                              q_start=[0, 8])
     assert_close(out2.float().cpu().numpy(), ref2, torch.bfloat16, "past capacity")
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("d", [64, 128])
+def test_token_major_matches_native_bitwise(gpu, kv_dtype, d):
+    """The reference's own cache layout ([NB, bs, Hkv, D] contiguous: V in
+    token rows) gives the native layout's output bit for bit: the same
+    operands reach the same products.  Seq 1's table holds an invalid (-1)
+    entry among its cached blocks, and every chunk ends inside a tile."""
+    print(f"[case] prefill token-major vs native kv={kv_dtype} d={d}", flush=True)
+    case = workloads.make_mixed_case(device=gpu, seed=21, chunks=[1, 33, 100], cached=[7, 250, 31],
+                                     decode_lens=[], num_q_heads=16, num_kv_heads=4, head_dim=d,
+                                     kv_dtype=kv_dtype)
+    t = workloads.materialize_mixed(case, "native")
+    _write_new_rows(case, t)
+    tables = [list(x) for x in case.prefill_tables]
+    tables[1][3] = -1
+    tab = workloads._int_tensor(tables, gpu)
+    out_native = _prefill(case, t, tables=tab)
+    tm = dict(t, k_cache=t["k_cache"].contiguous(), v_cache=t["v_cache"].contiguous())
+    assert tm["v_cache"].stride(1) == 4 * d and tm["v_cache"].stride(3) == 1
+    out_tok = _prefill(case, tm, tables=tab)
+    assert torch.equal(out_native, out_tok)
+    assert torch.isfinite(out_tok.float()).all()
 
 
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
