@@ -31,7 +31,7 @@ struct PrefillParams {
   // workspace
   int4* chunks;  // [N] {first q row, rows, position of the first row, row blocks before it}
   int4* items;   // [max_items] {chunk, row block, KV head, tiles}, longest first
-  int* header;   // {number of items, queue counter}
+  int* header;   // {items, shared queue counter, items in the per-XCD lists, 8 list counters}
 };
 
 // Query rows per work item for GQA group G.
