@@ -289,6 +289,31 @@ def test_long_single_sequence_split_over_many_waves(gpu, kv_dtype, n, hq, hkv, d
     assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, "long sequence")
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 4, 64), (32, 8, 128), (64, 8, 128), (16, 1, 64)])
+def test_merge_partial_counts(gpu, hq, hkv, d):
+    """One sequence of t tiles per KV head splits into about t partials per
+    head, so the lengths sweep the merge across its two paths: one partial,
+    the most its one-wave register path holds (64 / (G * D / 64)), and past
+    that (the chunked LDS path) up to four and more times as many."""
+    g_ = hq // hkv
+    kmax = 64 // (g_ * d // 64)
+    for tiles in sorted({1, kmax, kmax + 1, 2 * kmax + 1, 4 * kmax, 4 * kmax + 1, 4 * kmax + 3}):
+        n = 32 * tiles - 5
+        print(f"[case] merge partials hq={hq} hkv={hkv} d={d} tiles={tiles} n={n}", flush=True)
+        g = torch.Generator(device=gpu).manual_seed(tiles)
+        nb = (n + 15) // 16 + 3
+        perm = torch.randperm(nb, generator=torch.Generator().manual_seed(tiles)).tolist()
+        q = torch.randn(1, hq, d, generator=g, device=gpu).to(torch.bfloat16)
+        ksrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
+        vsrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
+        case = workloads.DecodeCase("parts", q, ksrc, vsrc, [perm[: (n + 15) // 16]], [n], 16, 1 / math.sqrt(d),
+                                    torch.float8_e4m3fn)
+        kc, vc, ks, vs = workloads.materialize(case, "paired")
+        out = _run(case, kc, vc, ks, vs, gpu)
+        ref = oracle_decode(case, kc, vc, ks, vs)
+        assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, f"{tiles} tiles")
+
+
 @pytest.mark.parametrize("kv_dtype,bs,d", [(torch.float32, 16, 64), (torch.float32, 16, 256), (torch.bfloat16, 8, 80)])
 def test_generic_path_many_partitions(gpu, kv_dtype, bs, d):
     """The generic (VALU) path on a small batch: the partition length shrinks
