@@ -852,6 +852,9 @@ bool prefill_supported(const PrefillParams& p, int q_dt, int kv_dt) {
   const bool token_major = p.k_s[3] == 1 && p.v_s[3] == 1 && p.v_s[1] != 1 && (p.k_s[1] * kb) % 16 == 0 &&
                            (p.v_s[1] * kb) % 16 == 0;
   if (!native && !token_major) return false;
+  // in-block offsets (15 token rows plus a row) are 32-bit in the kernel
+  const int64_t max_off = 16 * (p.k_s[1] > p.v_s[1] ? p.k_s[1] : p.v_s[1]) * kb + (int64_t)p.D * 16 * kb;
+  if (p.k_s[1] < 0 || p.v_s[1] < 0 || max_off >= ((int64_t)1 << 32)) return false;
   if ((p.k_s[0] * kb) % 16 || (p.k_s[2] * kb) % 16 || (p.v_s[0] * kb) % 16 || (p.v_s[2] * kb) % 16) return false;
   if (((uintptr_t)p.k & 15) || ((uintptr_t)p.v & 15)) return false;
   if (((uintptr_t)p.q & 15) || (p.q_sr * 2) % 16 || (p.q_sh * 2) % 16) return false;

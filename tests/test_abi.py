@@ -269,3 +269,35 @@ def test_shared_prefix_statement_is_validated():
         rc = lib.cf_paged_decode_shared(*(_abi.ref(d) for d in ds[:5]), _abi.ref(dsh), None, None, 0.125, 16, 512,
                                         _abi.ref(ds[5]), None, 0, None)
         assert rc == _abi.CF_ERR_INVALID and message in _abi.last_error()
+
+
+def test_prefill_cache_layout_checks():
+    """Chunked prefill's layout check, before any HIP call: the reference's
+    token-major caches pass it (the call then stops at the missing
+    workspace), a view whose token stride would overflow the kernel's 32-bit
+    in-block offsets is refused as unsupported, and so is a V tile that is
+    neither channel rows of 16 tokens nor token rows."""
+    lib = _abi.lib()
+    q = torch.zeros(4, 8, 64, dtype=torch.bfloat16)
+    cache = torch.zeros(10, 16, 2, 64, dtype=torch.bfloat16)  # [NB, bs, Hkv, D], token-major
+    bt = torch.zeros(1, 4, dtype=torch.int32)
+    sl = torch.tensor([4], dtype=torch.int32)
+    qs = torch.tensor([0, 4], dtype=torch.int32)
+    out = torch.zeros(4, 8, 64, dtype=torch.bfloat16)
+
+    def call(k, v):
+        ds = [_abi.descriptor(t) for t in (q, k, v, bt, sl, qs, out)]
+        for d in ds:
+            d.t.device = _abi.SFA_ROCM
+        return ds, lambda: lib.cf_prefill_chunk_fp8(*(_abi.ref(d) for d in ds[:6]), None, None, 0.125, 16,
+                                                    _abi.ref(ds[6]), None, 0, None)
+
+    ds, run = call(cache, cache)
+    assert run() == _abi.CF_ERR_WORKSPACE and "workspace" in _abi.last_error()
+    for i in (1, 2):
+        ds[i].t.r4.strides[1] = 1 << 28  # 16 rows x 2^28 elements x 2 bytes > 2^32
+    assert run() == _abi.CF_ERR_UNSUPPORTED and "token-major" in _abi.last_error()
+    # V with channel stride 1 and token stride 1 is no layout the kernel reads
+    ds, run = call(cache, cache)
+    ds[2].t.r4.strides[1] = 1
+    assert run() == _abi.CF_ERR_UNSUPPORTED
