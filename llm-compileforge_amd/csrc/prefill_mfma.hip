@@ -455,7 +455,9 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uniform(tid >> 6);
   const int li = lane & 15, lq = lane >> 4;
-  const int n_items = header[0], n_aff = header[2];
+  // list x is drained by the workgroups with blockIdx.x % 8 == x (wherever
+  // they run), so a grid of fewer than 8 takes every item from the queue
+  const int n_items = header[0], n_aff = gridDim.x >= kXcds ? header[2] : 0;
   const int cap = p.Mb * 16;
   // Beside the memory-bound decode kernel (a mixed step's two streams), a
   // SIMD holds one wave of each; the prefill's, on the step's critical path,
