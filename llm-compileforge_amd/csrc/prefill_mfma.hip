@@ -1,4 +1,4 @@
-// Chunked prefill over the paged KV cache (bf16 / e4m3fn, native layout).
+// Chunked prefill over the paged KV cache (bf16 / e4m3fn; native, paired or token-major).
 //
 // A chunk of L new query rows whose sequence now holds S tokens (its own
 // K/V already written to the cache) puts row i at position S - L + i; the
@@ -71,10 +71,10 @@ constexpr int kCostBins = 2048;   // tile counts at or above share the last bin
 constexpr int kXcds = 8;          // workgroup g runs on XCD g % 8, each with its own L2
 constexpr int kAffinePct = 75;    // share of the tiles taken from per-XCD lists
 
-__device__ __forceinline__ long long wave_incl_scan64(long long v, int lane) {
+__device__ __forceinline__ float wave_incl_scanf(float v, int lane) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const long long u = __shfl_up(v, o, 64);
+    const float u = __shfl_up(v, o, 64);
     if (lane >= o) v += u;
   }
   return v;
@@ -92,7 +92,7 @@ __device__ __forceinline__ int item_kvlen(int pos0, int rb, int RB, int L, int c
 __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillParams p) {
   __shared__ int hist[kCostBins];
   __shared__ int wave_tot[kPlanThreads / 64];
-  __shared__ long long wave_tiles[kPlanThreads / 64];
+  __shared__ float wave_tiles[kPlanThreads / 64];
   __shared__ int s_aff;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cap = p.Mb * 16;
@@ -140,28 +140,33 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillParam
     atomicAdd(&hist[kCostBins - 1 - min(tiles, kCostBins - 1)], p.Hkv);
   }
   __syncthreads();
-  // Exclusive scan of the bins (two per thread).
+  // Exclusive scans of the bins (two per thread): the items, and the
+  // tiles in them (bin b: kCostBins - 1 - b tiles per item; in float, as
+  // only the split point below depends on it).  The longest items, up to
+  // the first bin that reaches kAffinePct of all tiles, go to the per-XCD
+  // lists.
   const int h0 = hist[2 * tid], h1 = hist[2 * tid + 1];
+  const float t0 = (float)h0 * (float)(kCostBins - 1 - 2 * tid), t1 = (float)h1 * (float)(kCostBins - 2 - 2 * tid);
   const int incl = wave_incl_scan(h0 + h1, lane);
-  if (lane == 63) wave_tot[wave] = incl;
+  const float tincl = wave_incl_scanf(t0 + t1, lane);
+  if (lane == 63) {
+    wave_tot[wave] = incl;
+    wave_tiles[wave] = tincl;
+  }
   __syncthreads();
   int base = 0;
-  for (int w = 0; w < wave; ++w) base += wave_tot[w];
-  const int excl = base + incl - (h0 + h1);
-  const int total = base + incl;  // inclusive through this thread's bins
-  // The same scan over the tiles in the bins (bin b: kCostBins - 1 - b
-  // tiles per item): the longest items up to the first bin that reaches
-  // kAffinePct of all tiles go to the per-XCD lists.
-  const long long t0 = (long long)h0 * (kCostBins - 1 - 2 * tid), t1 = (long long)h1 * (kCostBins - 2 - 2 * tid);
-  const long long tincl = wave_incl_scan64(t0 + t1, lane);
-  if (lane == 63) wave_tiles[wave] = tincl;
-  __syncthreads();
-  long long tbase = 0, tall = 0;
+  float tbase = 0.0f, tall = 0.0f;
+#pragma unroll
   for (int w = 0; w < kPlanThreads / 64; ++w) {
-    if (w < wave) tbase += wave_tiles[w];
+    if (w < wave) {
+      base += wave_tot[w];
+      tbase += wave_tiles[w];
+    }
     tall += wave_tiles[w];
   }
-  const long long target = tall * kAffinePct / 100;
+  const int excl = base + incl - (h0 + h1);
+  const int total = base + incl;  // inclusive through this thread's bins
+  const float target = tall * (kAffinePct / 100.0f);
   if (h0 > 0 && tbase + tincl - t1 >= target) atomicMin(&s_aff, excl + h0);
   if (h1 > 0 && tbase + tincl >= target) atomicMin(&s_aff, excl + h0 + h1);
   __syncthreads();
