@@ -91,6 +91,33 @@ def test_shapes_match_oracle(gpu, hq, hkv, d, kv_dtype, layout):
     assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, f"prefill {hq}/{hkv}/{d}/{kv_dtype}")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_configurations(gpu, seed):
+    """Seeded random steps over every supported head shape, cache dtype and
+    layout: 1-6 chunks of 1-300 rows over cached prefixes of 0-2,000
+    tokens, so the work lists run from a handful of items (all on the
+    shared queue) to hundreds (per-XCD lists plus queue)."""
+    rng = np.random.default_rng(1000 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 2, 4, 8, 16]))
+    d = int(rng.choice([64, 128]))
+    kv_dtype = [torch.bfloat16, torch.float8_e4m3fn][int(rng.integers(2))]
+    layout = ["paired", "native", "token_major"][int(rng.integers(3))]
+    n = int(rng.integers(1, 7))
+    chunks = [int(x) for x in rng.integers(1, 301, n)]
+    cached = [int(x) for x in rng.integers(0, 2001, n)]
+    print(f"[case] random prefill seed={seed} hkv={hkv} g={g} d={d} kv={kv_dtype} layout={layout} "
+          f"chunks={chunks} cached={cached}", flush=True)
+    case = workloads.make_mixed_case(device=gpu, seed=seed, chunks=chunks, cached=cached, decode_lens=[],
+                                     num_q_heads=hkv * g, num_kv_heads=hkv, head_dim=d, kv_dtype=kv_dtype)
+    t = workloads.materialize_mixed(case, layout)
+    _write_new_rows(case, t)
+    out = _prefill(case, t)
+    ref, covered = oracle_prefill(case, t)
+    assert covered.all()
+    assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, f"random {seed}")
+
+
 @pytest.mark.parametrize("chunks,cached", [([512], [0]), ([512], [4096]), ([1] * 40, list(range(0, 4000, 100))),
                                            ([700, 3], [17, 9000])])
 def test_chunk_mixes(gpu, chunks, cached):
