@@ -317,6 +317,27 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
   }
 }
 
+// Token-major V staging: token row q of the tile sits at LDS row
+// vtok_slot(q), which puts the four token rows that one transposing read
+// takes (q = 8 k + 0..3, or 8 k + 4..7) at every other row: their 32-byte
+// pieces are then 8 banks apart (rows are 2 D + 16 bytes apart, 4 banks
+// per row) instead of 4 and overlapping.
+__device__ __forceinline__ int vtok_slot(int q) { return (q & ~7) | ((q & 3) << 1) | ((q >> 2) & 1); }
+
+// 16-bit V operand from the staged rows: channel 16 t + li of tokens
+// 8 lq .. 8 lq + 7 (the order vtok_operand16 gives, rows at vtok_slot).
+template <int D>
+__device__ __forceinline__ uint4 vtok_operand16_slots(const uint8_t* stage, int t, int li, int lq) {
+  constexpr int RS = vtok_row_stride<D, 2>();
+  const uint8_t* src = stage + (8 * lq + 2 * (li >> 2)) * RS + 32 * t + 8 * (li & 3);
+  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16_t*)((__attribute__((address_space(3))) const uint8_t*)src));
+  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16_t*)((__attribute__((address_space(3))) const uint8_t*)(src + RS)));
+  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+  return make_uint4(a.x, a.y, b.x, b.y);
+}
+
 // All ones when token r of block X (of a tile whose blocks' validity bits
 // are `ok`) is below `valid`, tile-relative, and its block is valid; else 0.
 __device__ __forceinline__ uint32_t vtok_keep_mask(int ok, int X, int r, int valid) {
@@ -367,7 +388,7 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
         const int X = u / (16 * Gm::VCPR), r = (u / Gm::VCPR) % 16, c = u % Gm::VCPR;
         const uint32_t km = full ? ~0u : vtok_keep_mask(t.ok, X, r, valid);
         const uint4 v = make_uint4(vr[i].x & km, vr[i].y & km, vr[i].z & km, vr[i].w & km);
-        uint8_t* row = rows + (16 * X + r) * Gm::VRS;
+        uint8_t* row = rows + vtok_slot(16 * X + r) * Gm::VRS;
         if constexpr (KT == kE4M3) {
           *(uint4*)(row + 32 * c) = __builtin_bit_cast(uint4, e4m3x8_to_f16(v.x, v.y));
           *(uint4*)(row + 32 * c + 16) = __builtin_bit_cast(uint4, e4m3x8_to_f16(v.z, v.w));
@@ -725,7 +746,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       qk(K1, a1, a2, s1b, s2b);
 #pragma unroll
       for (int t = 0; t < NV; ++t)
-        vraw[t] = VTOK ? vtok_operand16<D>((const uint8_t*)vl, t, li, lq) : vl[t * 64 + lane];
+        vraw[t] = VTOK ? vtok_operand16_slots<D>((const uint8_t*)vl, t, li, lq) : vl[t * 64 + lane];
       const float mta = lane_max(s1a, s2a);
       // keeps the max here, beside the MFMAs, instead of sunk past the
       // next branch to its use
