@@ -146,8 +146,11 @@ __device__ __forceinline__ void load_tile(TileRegs<KT, D, VTOK>& r, const KvCach
 //   words (4 elements) supplied by lanes 4j + L / 4 (j = 0..3).  Two reads per
 //   operand: for tokens 8 lq + 4 h .. + 3, lane (li, lq) points at token
 //   8 lq + 4 h + li / 4, channels 16 t + 4 (li % 4) .. + 3, and receives
-//   channel 16 t + li of those four tokens.
-// The row stride's 16-byte pad spreads the rows a group reads over the banks.
+//   channel 16 t + li of those four tokens.  Token row q is staged at row
+//   vtok_slot(q): the four rows one read takes are then every other row.
+// The row stride's 16-byte pad spreads the rows a group reads over the banks
+// (a 16-bit row then starts 4 banks after the previous one, so rows two
+// apart -- the 32-byte pieces one 16-bit read takes -- are 8 banks apart).
 template <int D, int KB = 1>
 constexpr int vtok_row_stride() {
   return D * KB + 16;
@@ -157,12 +160,18 @@ constexpr int vtok_stage_bytes() {
   return 32 * vtok_row_stride<D, KB>();
 }
 
+// Staging row of 16-bit token row q: rows 8 k + 0..3 go to the even rows
+// of 8 k .. 8 k + 7, rows 8 k + 4..7 to the odd ones.
+__device__ __forceinline__ int vtok_slot(int q) { return (q & ~7) | ((q & 3) << 1) | ((q >> 2) & 1); }
+
 template <int D, int KB = 1>
 __device__ __forceinline__ void vtok_stage(uint8_t* stage, const uint4* v, int lane) {
   constexpr int LPR = D * KB / 16, RPI = 64 / LPR, NVR = 32 * D * KB / (64 * 16);
 #pragma unroll
-  for (int i = 0; i < NVR; ++i)
-    *(uint4*)(stage + (lane / LPR + RPI * i) * vtok_row_stride<D, KB>() + (lane % LPR) * 16) = v[i];
+  for (int i = 0; i < NVR; ++i) {
+    const int q = lane / LPR + RPI * i;
+    *(uint4*)(stage + (KB == 2 ? vtok_slot(q) : q) * vtok_row_stride<D, KB>() + (lane % LPR) * 16) = v[i];
+  }
 }
 
 typedef int v2i32_t __attribute__((ext_vector_type(2)));
@@ -177,15 +186,16 @@ __device__ __forceinline__ uint2 vtok_operand(const uint8_t* stage, int t, int l
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
-// 16-bit V: channel 16 t + li of tokens 8 lq .. 8 lq + 7 (8 elements).
+// 16-bit V: channel 16 t + li of tokens 8 lq .. 8 lq + 7 (8 elements), rows
+// at vtok_slot.
 template <int D>
 __device__ __forceinline__ uint4 vtok_operand16(const uint8_t* stage, int t, int li, int lq) {
   constexpr int RS = vtok_row_stride<D, 2>();
-  const uint8_t* src = stage + (8 * lq + (li >> 2)) * RS + 32 * t + 8 * (li & 3);
+  const uint8_t* src = stage + (8 * lq + 2 * (li >> 2)) * RS + 32 * t + 8 * (li & 3);
   const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) v4i16_t*)((__attribute__((address_space(3))) const uint8_t*)src));
   const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4i16_t*)((__attribute__((address_space(3))) const uint8_t*)(src + 4 * RS)));
+      (__attribute__((address_space(3))) v4i16_t*)((__attribute__((address_space(3))) const uint8_t*)(src + RS)));
   const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
   return make_uint4(a.x, a.y, b.x, b.y);
 }

@@ -213,7 +213,7 @@ struct Geo {
   static constexpr int VPT = (VU + 255) / 256;
   // Token-major V (the reference's [NB, bs, Hkv, D] layout): a 16-byte load
   // is VCH channels of one token; the tile is staged as 32 rows of 16-bit
-  // values, RS bytes apart (16 bytes of padding: no bank conflicts), and
+  // values, RS bytes apart at rows vtok_slot (no bank conflicts on the reads), and
   // read back transposed into the operand order.
   static constexpr int VCH = 16 / KB;                  // channels per load
   static constexpr int VCPR = D / VCH;                 // loads per token row
@@ -317,27 +317,6 @@ __device__ __forceinline__ void stage_load(uint4* kr, uint4* vr, const PrefillPa
   }
 }
 
-// Token-major V staging: token row q of the tile sits at LDS row
-// vtok_slot(q), which puts the four token rows that one transposing read
-// takes (q = 8 k + 0..3, or 8 k + 4..7) at every other row: their 32-byte
-// pieces are then 8 banks apart (rows are 2 D + 16 bytes apart, 4 banks
-// per row) instead of 4 and overlapping.
-__device__ __forceinline__ int vtok_slot(int q) { return (q & ~7) | ((q & 3) << 1) | ((q >> 2) & 1); }
-
-// 16-bit V operand from the staged rows: channel 16 t + li of tokens
-// 8 lq .. 8 lq + 7 (the order vtok_operand16 gives, rows at vtok_slot).
-template <int D>
-__device__ __forceinline__ uint4 vtok_operand16_slots(const uint8_t* stage, int t, int li, int lq) {
-  constexpr int RS = vtok_row_stride<D, 2>();
-  const uint8_t* src = stage + (8 * lq + 2 * (li >> 2)) * RS + 32 * t + 8 * (li & 3);
-  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4i16_t*)((__attribute__((address_space(3))) const uint8_t*)src));
-  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4i16_t*)((__attribute__((address_space(3))) const uint8_t*)(src + RS)));
-  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
-  return make_uint4(a.x, a.y, b.x, b.y);
-}
-
 // All ones when token r of block X (of a tile whose blocks' validity bits
 // are `ok`) is below `valid`, tile-relative, and its block is valid; else 0.
 __device__ __forceinline__ uint32_t vtok_keep_mask(int ok, int X, int r, int valid) {
@@ -375,7 +354,8 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
   // the masking (a wave-uniform branch).
   const bool full = FULL || (valid >= 32 && t.ok == 3);
   if constexpr (VTOK) {
-    // token row 16 X + r of the staged tile, 16-bit; a token past `valid`
+    // token row 16 X + r of the staged tile, 16-bit, at row vtok_slot of
+    // it (the order vtok_operand16 reads); a token past `valid`
     // or in an invalid block is written as zeros.  The keep mask is formed
     // arithmetically: written as a short-circuit select, the ROCm 7.2
     // compiler dropped the keep lanes' copy of the loaded value (bf16,
@@ -746,7 +726,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       qk(K1, a1, a2, s1b, s2b);
 #pragma unroll
       for (int t = 0; t < NV; ++t)
-        vraw[t] = VTOK ? vtok_operand16_slots<D>((const uint8_t*)vl, t, li, lq) : vl[t * 64 + lane];
+        vraw[t] = VTOK ? vtok_operand16<D>((const uint8_t*)vl, t, li, lq) : vl[t * 64 + lane];
       const float mta = lane_max(s1a, s2a);
       // keeps the max here, beside the MFMAs, instead of sunk past the
       // next branch to its use
