@@ -5,8 +5,8 @@ straight from CacheManager slabs.
 Writes and reads are bit-exact against the CPU oracle (oracle/
 cache_manager.py, oracle/fp8.py) and torch's CPU dtype casts (the
 reference's slab assignment casts with torch).  Attention is compared with
-the float64 oracle at the decode tolerance (max-abs 2e-2 / bf16 ulp,
-cosine >= 0.9999; tests/gpu_util.py).
+the float64 oracle at the decode tolerance (max-abs 2e-2 against the
+exact value rounded to bf16, cosine >= 0.9999; tests/gpu_util.py).
 """
 
 from __future__ import annotations

@@ -6,7 +6,7 @@ size-independent properties: every prefill row equals the decode kernel
 run with the row's truncated length (the semantics' own reduction), the
 written FP8 codes equal the oracle encoder's bit for bit, and a sample of
 rows and decodes matches the float64 oracle.  Tolerances: bf16 outputs
-within max(2e-2, 1 bf16 ulp) of the exact value, cosine >= 0.9999.
+within 2e-2 of the exact value rounded to bf16, cosine >= 0.9999.
 """
 
 from __future__ import annotations
@@ -218,11 +218,13 @@ def test_repeated_calls_shrinking(gpu):
     assert_close(os_.float().cpu().numpy(), oracle_prefill(small, ts)[0], torch.bfloat16, "small")
 
 
-def test_c5_full_step(gpu):
-    """The full c5 step: write, decode, prefill on one stream."""
-    print("[case] c5 full step", flush=True)
+@pytest.mark.parametrize("layout", ["paired", "token_major"])
+def test_c5_full_step(gpu, layout):
+    """The full c5 step: write, decode, prefill on one stream (the
+    benchmarked paired layout, and the reference's own token-major one)."""
+    print(f"[case] c5 full step layout={layout}", flush=True)
     case = workloads.make_mixed_case(device=gpu, seed=0)
-    t = workloads.materialize_mixed(case)
+    t = workloads.materialize_mixed(case, layout)
     _write_new_rows(case, t)
     dec = paged_attention_tensors(t["q_decode"], t["k_cache"], t["v_cache"], t["decode_tables"], t["decode_lens"],
                                   16, case.scale, k_scale=t["k_scale"], v_scale=t["v_scale"])

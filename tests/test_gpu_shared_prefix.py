@@ -5,7 +5,7 @@ MFMA decode reads them (once per group of up to 16/G sharers), never the
 result: every case is checked against the float64 oracle on the exact
 cache contents, and against the same call without the statement.
 Tolerances as elsewhere: bf16 outputs cosine >= 0.9999 and each element
-within max(2e-2, one bf16 ulp of the exact value).
+within 2e-2 of the exact value rounded to bf16.
 """
 
 from __future__ import annotations
