@@ -476,6 +476,9 @@ def main() -> None:
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--partition", type=int, default=512)
     ap.add_argument("--layout", default="paired")
+    ap.add_argument("--q-dtype", choices=["bf16", "float16", "float32"], default=None,
+                    help="cast the decode queries (fp16 takes the MFMA kernel's fp16 operands, fp32 the generic "
+                         "kernel); the line then names its own metric")
     ap.add_argument("--pools", type=int, default=2, help="cache copies rotated between steps")
     ap.add_argument("--cpu-sample", type=int, default=8)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -514,6 +517,8 @@ def main() -> None:
         print(json.dumps(result), flush=True)
         return
     case = workloads.make_case(args.config, device=dev, seed=0, batch=args.batch)
+    if args.q_dtype is not None:
+        case.q = case.q.to({"bf16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}[args.q_dtype])
     pools = []
     for i in range(args.pools):
         pools.append(workloads.materialize(case, args.layout))
@@ -636,8 +641,9 @@ def main() -> None:
     q_short = short[case.q.dtype][1]
     result = {
         # BASELINE.json's metric for its config (c3); other configs name theirs
-        "metric": METRIC if args.config == "c3_llama3_8b" else
-        f"paged-decode tokens/s + HBM GB/s (% peak), {args.config} {kv_name} KV, 1 MI355X",
+        "metric": METRIC if args.config == "c3_llama3_8b" and args.q_dtype is None else
+        f"paged-decode tokens/s + HBM GB/s (% peak), {args.config} {kv_name} KV"
+        + (f" / {q_short} q" if args.q_dtype is not None else "") + ", 1 MI355X",
         "value": case.batch / (ms_step / 1e3),
         "unit": "tokens/s",
         "n_gpus": 1,
