@@ -394,15 +394,24 @@ int32_t cf_copy_blocks(CfTensor* cache, const CfTensor* pairs, void* stream);
 
 /* Kernel timing hook for benchmarks (no reference counterpart).  While
  * enabled, every kernel this library launches carries a pair of HIP events
- * that the launch itself stamps with the kernel's start and end
- * (hipExtLaunchKernel: no marker packets are added to the stream, so the
- * kernels run back to back as they do without the hook).  cf_profile_query
- * synchronizes on the recorded events and returns the summed duration (ms)
- * and launch count of kernels whose name starts with `prefix`. */
+ * that hipExtLaunchKernel records at the kernel's start and end on the
+ * launch stream; a launch the runtime rejects leaves no record.  Stamping
+ * is not free: each stamped launch adds host work and a completion signal,
+ * so a stamped pass runs a few us per launch slower than an unstamped one
+ * and is no step timing.  Events come from a pool; cf_profile_reserve
+ * creates them ahead of a measured pass (an event created inside it costs
+ * host time, lets the GPU idle between launches and lengthens the kernels
+ * that follow an idle gap).  cf_profile_query synchronizes on the recorded
+ * events and returns the summed duration (ms) and launch count of kernels
+ * whose name starts with `prefix`; cf_profile_durations writes up to `cap`
+ * of those durations (ms, launch order) and their total count. */
 int32_t cf_profile_enable(int32_t on);
 int32_t cf_profile_reset(void);
+int32_t cf_profile_reserve(int64_t events);
 int32_t cf_profile_query(const char* prefix, double* total_ms,
                          int64_t* launches);
+int32_t cf_profile_durations(const char* prefix, float* ms, int64_t cap,
+                             int64_t* launches);
 
 #ifdef __cplusplus
 }

@@ -203,6 +203,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int32,
         [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)],
     ),
+    "cf_profile_reserve": (ctypes.c_int32, [ctypes.c_int64]),
+    "cf_profile_durations": (
+        ctypes.c_int32,
+        [ctypes.c_char_p, ctypes.c_void_p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)],
+    ),
 }
 
 

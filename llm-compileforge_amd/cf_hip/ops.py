@@ -588,6 +588,20 @@ class KernelTimer:
         return float(ms.value), int(n.value)
 
     @staticmethod
+    def durations(prefix: str) -> list[float]:
+        """Per-launch durations (ms, launch order) of kernels named `prefix`*."""
+        n = ctypes.c_int64(0)
+        check(lib().cf_profile_durations(prefix.encode(), None, 0, ctypes.byref(n)), "cf_profile_durations")
+        buf = (ctypes.c_float * max(n.value, 1))()
+        check(lib().cf_profile_durations(prefix.encode(), buf, n.value, ctypes.byref(n)), "cf_profile_durations")
+        return [float(buf[i]) for i in range(n.value)]
+
+    @staticmethod
+    def reserve(events: int) -> None:
+        """Creates timing events ahead of a measured pass (two per launch)."""
+        check(lib().cf_profile_reserve(int(events)), "cf_profile_reserve")
+
+    @staticmethod
     def reset() -> None:
         lib().cf_profile_reset()
 

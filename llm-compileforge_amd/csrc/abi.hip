@@ -75,6 +75,7 @@ bool g_prof_on = false;
 std::vector<ProfRecord> g_prof_records;
 std::vector<hipEvent_t> g_prof_pool;
 
+// Callers hold g_prof_mu.
 hipEvent_t take_event() {
   if (!g_prof_pool.empty()) {
     hipEvent_t e = g_prof_pool.back();
@@ -85,24 +86,23 @@ hipEvent_t take_event() {
   if (hipEventCreate(&e) != hipSuccess) return nullptr;
   return e;
 }
-}  // namespace
 
-bool profiling_enabled() { return g_prof_on; }
-
-namespace {
 // Events armed by a ProfileScope for this thread's next launch.
 struct Pending {
-  std::string name;
+  const char* name = nullptr;
   hipEvent_t begin = nullptr, end = nullptr;
 };
 thread_local Pending g_pending;
 
+// Callers hold g_prof_mu.
 void release_pending() {
   if (g_pending.begin) g_prof_pool.push_back(g_pending.begin);
   if (g_pending.end) g_prof_pool.push_back(g_pending.end);
   g_pending = Pending{};
 }
 }  // namespace
+
+bool profiling_enabled() { return g_prof_on; }
 
 void profile_arm(const char* name) {
   if (!g_prof_on) return;
@@ -125,19 +125,25 @@ void profile_disarm() {
   release_pending();
 }
 
-hipEvent_t profile_take_begin() {
-  if (!g_pending.begin) return nullptr;
-  std::lock_guard<std::mutex> lock(g_prof_mu);
-  g_prof_records.push_back(ProfRecord{g_pending.name, g_pending.begin, g_pending.end});
-  hipEvent_t b = g_pending.begin;
-  g_pending.begin = nullptr;
-  return b;
+ArmedEvents profile_take() {
+  ArmedEvents ev;
+  if (!g_pending.begin) return ev;
+  ev.name = g_pending.name;
+  ev.begin = g_pending.begin;
+  ev.end = g_pending.end;
+  g_pending = Pending{};
+  return ev;
 }
 
-hipEvent_t profile_take_end() {
-  hipEvent_t e = g_pending.end;
-  g_pending = Pending{};
-  return e;
+void profile_commit(const ArmedEvents& ev, bool launched) {
+  if (!ev.begin) return;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  if (launched) {
+    g_prof_records.push_back(ProfRecord{ev.name, ev.begin, ev.end});
+  } else {
+    g_prof_pool.push_back(ev.begin);
+    if (ev.end) g_prof_pool.push_back(ev.end);
+  }
 }
 
 namespace {
@@ -832,6 +838,38 @@ int32_t cf_profile_query(const char* prefix, double* total_ms, int64_t* launches
     ++n;
   }
   *total_ms = sum;
+  *launches = n;
+  return CF_OK;
+}
+
+int32_t cf_profile_reserve(int64_t events) {
+  CF_CHECK(events >= 0 && events <= (1 << 20), "cf_profile_reserve: %lld events out of range", (long long)events);
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  while ((int64_t)g_prof_pool.size() < events) {
+    hipEvent_t e = nullptr;
+    CF_HIP_CHECK(hipEventCreate(&e));
+    g_prof_pool.push_back(e);
+  }
+  return CF_OK;
+}
+
+int32_t cf_profile_durations(const char* prefix, float* ms, int64_t cap, int64_t* launches) {
+  CF_CHECK(prefix != nullptr && launches != nullptr, "NULL argument");
+  CF_CHECK(cap >= 0 && (cap == 0 || ms != nullptr), "cf_profile_durations: NULL output for %lld entries",
+           (long long)cap);
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  int64_t n = 0;
+  const size_t plen = std::strlen(prefix);
+  for (auto& r : g_prof_records) {
+    if (r.name.compare(0, plen, prefix) != 0) continue;
+    if (n < cap) {
+      CF_HIP_CHECK(hipEventSynchronize(r.end));
+      float d = 0.0f;
+      CF_HIP_CHECK(hipEventElapsedTime(&d, r.begin, r.end));
+      ms[n] = d;
+    }
+    ++n;
+  }
   *launches = n;
   return CF_OK;
 }

@@ -84,29 +84,43 @@ int32_t view_of(const CfTensor* t, const char* name, int rank, View* v);
 // ---- launch profiling ---------------------------------------------------
 // While the timing hook (cf_profile_enable) is on, a ProfileScope arms a
 // pair of HIP events for the next CF_LAUNCH on this thread.  The launch
-// hands them to hipExtLaunchKernel, which stamps them with the kernel's own
-// start and end (no marker packets are added to the stream), so the
-// measured duration is the kernel's execution time.
+// hands them to hipExtLaunchKernel, which records them at the kernel's
+// start and end on its stream; the pair becomes a launch record only when
+// the runtime accepted the launch, and goes back to the pool otherwise.
 bool profiling_enabled();
 // Arms events for kernel `name` (no-op when profiling is off).
 void profile_arm(const char* name);
 // Disarms events the launch did not consume (error paths).
 void profile_disarm();
-// The armed events (nullptr when none); registers the launch's record.
-hipEvent_t profile_take_begin();
-hipEvent_t profile_take_end();
+
+struct ArmedEvents {
+  const char* name = nullptr;
+  hipEvent_t begin = nullptr, end = nullptr;
+};
+// Hands over this thread's armed events (all null when none are armed).
+ArmedEvents profile_take();
+// Registers the launch record when `launched`, else returns the events to
+// the pool.  No-op for an empty pair.
+void profile_commit(const ArmedEvents& ev, bool launched);
 
 struct ProfileScope {
   ProfileScope(const char* name, hipStream_t) { profile_arm(name); }
   ~ProfileScope() { profile_disarm(); }
 };
 
-// Kernel launch on `stream`, carrying the armed timing events if any.
-#define CF_LAUNCH(kernel, grid, block, lds, stream, ...)                                                \
-  do {                                                                                                 \
-    hipEvent_t cf_b_ = ::cf::profile_take_begin();                                                     \
-    hipEvent_t cf_e_ = ::cf::profile_take_end();                                                       \
-    hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, cf_b_, cf_e_, 0, __VA_ARGS__);              \
+// Kernel launch on `stream`: an ordinary launch (what stream capture
+// records), or, when timing events are armed, hipExtLaunchKernel carrying
+// them.  The launch's error stays pending for the caller's hipGetLastError
+// check.
+#define CF_LAUNCH(kernel, grid, block, lds, stream, ...)                                                  \
+  do {                                                                                                   \
+    const ::cf::ArmedEvents cf_ev_ = ::cf::profile_take();                                               \
+    if (cf_ev_.begin) {                                                                                  \
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, cf_ev_.begin, cf_ev_.end, 0, __VA_ARGS__); \
+      ::cf::profile_commit(cf_ev_, hipPeekAtLastError() == hipSuccess);                                  \
+    } else {                                                                                             \
+      hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                                 \
+    }                                                                                                    \
   } while (0)
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -49,7 +49,7 @@ _logger = logging.getLogger(__name__)
 _ROLE_KEY, _ROLE_VALUE, _ROLE_PLAIN = "k", "v", "plain"
 
 
-# ── Policy ────────────────────────────────────────────────────────────
+# Cache policy types (the reference's proto-backed dataclasses).
 
 
 def _dict_to_proto_cache_policy(raw: dict[str, Any]) -> SfaCachePolicy:
@@ -115,7 +115,7 @@ def _dtype_from_str(name: str) -> torch.dtype:
     return mapping.get(name, torch.float32)
 
 
-# ── Host-side addressing (pure functions, no device work) ─────────────
+# Host-side addressing: pure functions, no device work.
 
 
 def first_cover_table(block_tables: dict[str, list[int]], num_blocks: int) -> np.ndarray:
@@ -240,7 +240,7 @@ def _slab_role(spec: Any, intercepts: list[Any]) -> str:
     return _ROLE_PLAIN
 
 
-# ── CacheManager ──────────────────────────────────────────────────────
+# The slab owner.
 
 
 class CacheManager:
@@ -311,7 +311,7 @@ class CacheManager:
             return torch.zeros(self._max_requests, L, D, dtype=dtype, device=self._device)
         raise ValueError(f"Unknown storage type: {spec.slab_type}")
 
-    # ── Per-step state ────────────────────────────────────
+    # Step bookkeeping: the active request and its positions.
 
     def begin_step(self, block_tables: dict[str, list[int]]) -> None:
         """Sets this step's block tables and resets the layer counters."""
@@ -341,7 +341,7 @@ class CacheManager:
             self._sorted = (ids, torch.from_numpy(mat).to(self._device), lens)
         return self._sorted
 
-    # ── FP8 scales ────────────────────────────────────────
+    # Per-(layer, KV head) FP8 dequant scales of the paged slabs.
 
     def kv_scales(self, slab_id: str) -> torch.Tensor:
         """Per-(layer, head) float32 dequant scales [L, H] of an FP8 slab."""
@@ -371,7 +371,7 @@ class CacheManager:
         self.kv_scales(slab_id)[layer_idx].copy_(sc.reshape(-1))
         return sc
 
-    # ── Paged KV I/O ──────────────────────────────────────
+    # Writing and reading K/V rows through block tables.
 
     def layer_view(self, slab_id: str, layer_idx: int) -> torch.Tensor:
         """Layer `layer_idx` of a paged slab as [num_blocks, block_size, heads, dim]."""
@@ -431,7 +431,7 @@ class CacheManager:
         sc = self._scales[slab_id][layer_idx] if slab_id in self._scales else None
         return _ops.paged_gather(view, tables, int(max_seq_len), scale=sc)
 
-    # ── Attention over the slabs ──────────────────────────
+    # Decode and chunked-prefill attention straight over the slabs.
 
     def attend(
         self,
@@ -565,7 +565,7 @@ class CacheManager:
         """Every paged slab (all layers), e.g. for BlockManager.copy_blocks."""
         return [t for name, t in self._slabs.items() if self._specs[name].slab_type == "paged"]
 
-    # ── Fixed state I/O ──────────────────────────────────
+    # Fixed-size (per-slot) state slabs: [slots, layers, ...] rows.
 
     def write_fixed(self, slab_id: str, slot: int, layer_idx: int, data: torch.Tensor) -> None:
         slab = self._slabs[slab_id]
@@ -574,41 +574,37 @@ class CacheManager:
     def read_fixed(self, slab_id: str, slot: int, layer_idx: int) -> torch.Tensor:
         return self._slabs[slab_id][slot, layer_idx]
 
-    # ── Helpers ───────────────────────────────────────────
-
     def _normalize_kv(self, data: torch.Tensor, slab_id: str) -> torch.Tensor:
         spec = self._specs[slab_id]
         return normalize_kv(data, spec.num_heads, spec.head_dim)
 
     @staticmethod
     def _pos_to_list(positions: torch.Tensor) -> list[int]:
-        if positions.dim() >= 1:
-            return [int(p) for p in positions.flatten().tolist()]
-        return [int(positions.item())]
+        """Token positions as Python ints, in order (a 0-d tensor gives one)."""
+        return [int(v) for v in positions.reshape(-1).tolist()]
 
-    # ── Slab info ─────────────────────────────────────────
+    # Policy-derived geometry (reference cache_manager.py:241-267): the
+    # first positive value among the policy's slabs, paged slabs only for
+    # the head geometry; 0 when no slab states it.
+
+    def _policy_value(self, field: str, paged_only: bool) -> int:
+        values = (int(getattr(spec, field)) for spec in self._policy.slabs
+                  if not paged_only or spec.slab_type == "paged")
+        return next((v for v in values if v > 0), 0)
 
     @property
     def has_paged_cache(self) -> bool:
-        return any(s.slab_type == "paged" for s in self._policy.slabs)
+        """Whether the policy declares at least one paged (block-table) slab."""
+        return any(spec.slab_type == "paged" for spec in self._policy.slabs)
 
     def configured_kv_heads(self) -> int:
-        for spec in self._policy.slabs:
-            if spec.slab_type == "paged" and spec.num_heads > 0:
-                return int(spec.num_heads)
-        return 0
+        return self._policy_value("num_heads", paged_only=True)
 
     def configured_head_dim(self) -> int:
-        for spec in self._policy.slabs:
-            if spec.slab_type == "paged" and spec.head_dim > 0:
-                return int(spec.head_dim)
-        return 0
+        return self._policy_value("head_dim", paged_only=True)
 
     def configured_num_layers(self) -> int:
-        for spec in self._policy.slabs:
-            if spec.num_layers > 0:
-                return int(spec.num_layers)
-        return 0
+        return self._policy_value("num_layers", paged_only=False)
 
 
 __all__ = [

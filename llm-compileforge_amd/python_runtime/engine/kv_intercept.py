@@ -6,8 +6,9 @@ dense SDPA call that follows it (python_runtime/engine/mlir_executor.py
   1. writes the op's K and V operands into the paged slabs at this step's
      positions (CacheManager.write_paged, one Python loop per token);
   2. on a decode step, gathers each slab's rows [0, max_position] back into
-     dense [requests, heads, seq, dim] tensors (read_paged) and substitutes
-     them for the SDPA's K and V operands;
+     dense [requests, heads, seq, dim] tensors (read_paged: requests in
+     sorted id order, rows past a request's table left zero) and
+     substitutes them for the SDPA's K and V operands;
   3. runs the SDPA op densely through the HAL (hal.execute).
 
 PagedKVIntercept keeps the intercept's rules -- which intercepts apply
@@ -15,20 +16,28 @@ PagedKVIntercept keeps the intercept's rules -- which intercepts apply
 sequential layer resolution, the write placement -- and replaces the data
 path:
   - the writes are one cf_paged_write launch per slab;
-  - decode: nothing is gathered; `run_sdpa` computes the op's output with
-    the paged decode kernel straight from the slabs (CacheManager.attend),
-    over exactly the prefix through the fed token (max_position + 1 tokens,
-    cut to each request's table);
-  - prefill: the SDPA inputs stay untouched (as in the reference); with
-    bf16 queries over bf16 / e4m3 slabs and a single request, `run_sdpa`
-    runs chunked-prefill attention from the slabs (CacheManager
-    .attend_chunks: the row at position p sees positions [0, p]), which for
-    a prefill starting at position 0 is exactly the reference's causal
-    dense SDPA, and for a later chunk also sees the cached prefix; other
-    prefill calls go to the HAL unchanged.
-With replace_inputs=True the decode step instead does what the reference
-does -- gather (one cf_paged_gather launch per slab) and substitute the SDPA
-operands -- and `run_sdpa` passes the op to the HAL.
+  - decode: when every request's table covers max_position + 1 tokens,
+    nothing is gathered; `run_sdpa` computes the op's output with the paged
+    decode kernel straight from the slabs (CacheManager.attend), each
+    request over exactly the prefix through the fed token, which is what
+    the reference's gathered operands hold.  When some table is shorter,
+    the reference's gather pads that request with zero rows that take part
+    in its softmax; such a step gathers and substitutes the operands as the
+    reference does and the op runs on the HAL, so its output is the
+    reference's in every case;
+  - prefill: the SDPA inputs stay untouched and the op runs on the HAL, as
+    in the reference (dense attention over the op's own K and V with its
+    positional mask).  With prefill_from_slabs=True, a single request's
+    causal chunk with bf16 queries over bf16 / e4m3 slabs runs
+    chunked-prefill attention from the slabs instead (CacheManager
+    .attend_chunks: the row at position p sees positions [0, p]).  That is
+    a different operation, not a faster route to the same one: it reads K
+    and V back from the slabs (on e4m3 slabs, the quantized values) and a
+    chunk after the first also sees the cached prefix, which the
+    reference's call never does.
+With replace_inputs=True every decode step gathers (one cf_paged_gather
+launch per slab) and substitutes the SDPA operands, and `run_sdpa` passes
+the op to the HAL.
 
 An op is any object with `op_name`, `operands`, `results` and (optionally)
 `attributes`, as the reference's compiler.artifact.MlirOp.
@@ -68,12 +77,17 @@ class PagedKVIntercept:
             (mlir_executor.py:105-109).
         replace_inputs: decode as the reference does (gather + substitute
             the SDPA operands) instead of attending from the slabs.
+        prefill_from_slabs: answer causal single-request prefill chunks
+            with chunked-prefill attention over the slabs (which sees the
+            cached prefix and the slabs' quantized values) instead of the
+            reference's dense SDPA over the op's own K and V.
     """
 
     def __init__(self, cache_mgr: CacheManager, intercepts: list[Any], ssa_producer: dict[str, tuple[int, int]],
-                 replace_inputs: bool = False) -> None:
+                 replace_inputs: bool = False, prefill_from_slabs: bool = False) -> None:
         self.cache_mgr = cache_mgr
         self.replace_inputs = replace_inputs
+        self.prefill_from_slabs = prefill_from_slabs
         self._by_op: dict[str, list[Any]] = {}
         for idef in intercepts:
             self._by_op.setdefault(idef.op_name_pattern, []).append(idef)
@@ -86,7 +100,7 @@ class PagedKVIntercept:
 
     @classmethod
     def from_module(cls, module: Any, device: torch.device | str | None = None,
-                    replace_inputs: bool = False) -> "PagedKVIntercept | None":
+                    replace_inputs: bool = False, prefill_from_slabs: bool = False) -> "PagedKVIntercept | None":
         """Built from a compiled module the way the reference executor sets
         up its cache manager (mlir_executor.py:105-123): the metadata's
         cache_policy and num_blocks, the functions' outputs as producers.
@@ -105,7 +119,7 @@ class PagedKVIntercept:
                 producer[name.lstrip("%")] = (fi, oi)
         num_blocks = int(module.metadata.get("num_blocks", _DEFAULT_NUM_BLOCKS))
         mgr = CacheManager(policy, num_blocks=num_blocks, device=device)
-        return cls(mgr, list(policy.intercepts), producer, replace_inputs)
+        return cls(mgr, list(policy.intercepts), producer, replace_inputs, prefill_from_slabs)
 
     # ── per-step state (the executor's _block_tables / _current_*) ───────
 
@@ -158,8 +172,12 @@ class PagedKVIntercept:
                 continue
             if positions is None or positions.numel() == 0:
                 continue
-            if self.is_decode and self.replace_inputs:
-                seq_len = int(positions.max().item()) + 1
+            if not self.is_decode:
+                if self.prefill_from_slabs:
+                    self._pending.setdefault(self._op_key(op), {})[src_idx] = (idef.slab_id, layer)
+                continue
+            seq_len = int(positions.max().item()) + 1
+            if self.replace_inputs or not self._tables_cover(seq_len):
                 gathered = self.cache_mgr.read_paged(idef.slab_id, layer, seq_len)
                 key = op.operands[src_idx]
                 key = key if key in ssa_values else key.lstrip("%")
@@ -170,6 +188,12 @@ class PagedKVIntercept:
                     ssa_values[key] = gathered.to(dtype)
                 continue
             self._pending.setdefault(self._op_key(op), {})[src_idx] = (idef.slab_id, layer)
+
+    def _tables_cover(self, seq_len: int) -> bool:
+        """Whether every request's table holds seq_len tokens, i.e. the
+        reference's gather would add no zero rows."""
+        bs = self.cache_mgr._block_size
+        return all(len(t) * bs >= seq_len for t in self.block_tables.values())
 
     @staticmethod
     def _source(idef: Any, op: Any, ssa_values: dict[str, torch.Tensor]) -> torch.Tensor | None:
@@ -188,38 +212,90 @@ class PagedKVIntercept:
 
     def run_sdpa(self, op: Any, inputs: list[torch.Tensor], hal: Any, **attrs: Any) -> torch.Tensor:
         """The op's output: attention from the slabs when `handle` recorded
-        both K (operand 1) and V (operand 2) for it, else hal.execute(...)
-        on `inputs` as the reference does."""
+        both K (operand 1) and V (operand 2) for it and the call is one the
+        kernels compute exactly as the reference's dense SDPA would, else
+        hal.execute(...) as the reference does -- on a decode step over the
+        operands the reference's gather would substitute."""
         pending = self._pending.pop(self._op_key(op), None)
         if pending is not None and 1 in pending and 2 in pending and inputs and inputs[0].dim() == 4:
             (k_slab, k_layer), (v_slab, v_layer) = pending[1], pending[2]
             if k_layer == v_layer:
-                out = (self._decode(inputs[0], k_slab, v_slab, k_layer, attrs) if self.is_decode
-                       else self._prefill(inputs[0], k_slab, v_slab, k_layer, attrs))
+                if self.is_decode:
+                    out = self._decode(inputs, k_slab, v_slab, k_layer, attrs)
+                    if out is None:
+                        inputs = self._gathered(inputs, pending)
+                else:
+                    out = self._prefill(inputs, k_slab, v_slab, k_layer, attrs)
                 if out is not None:
                     return out
         return hal.execute(op.op_name, inputs, **attrs)
 
-    def _decode(self, q: torch.Tensor, k_slab: str, v_slab: str, layer: int, attrs: dict) -> torch.Tensor | None:
+    def _gathered(self, inputs: list[torch.Tensor], pending: dict[int, tuple[str, int]]) -> list[torch.Tensor]:
+        """`inputs` with K and V replaced as the reference's decode intercept
+        replaces them: rows [0, max_position] of every request (sorted ids)
+        gathered from the slabs, zero past a request's table."""
+        seq_len = int(self.positions.max().item()) + 1
+        out = list(inputs)
+        for idx in (1, 2):
+            slab, layer = pending[idx]
+            g = self.cache_mgr.read_paged(slab, layer, seq_len)
+            if g.dim() == 4:
+                g = g.permute(0, 2, 1, 3)
+            out[idx] = g.to(inputs[idx].dtype)
+        return out
+
+    @staticmethod
+    def _mask_of(inputs: list[torch.Tensor], attrs: dict) -> torch.Tensor | None:
+        mask = attrs.get("attn_mask")
+        if mask is None and len(inputs) > 3:
+            mask = inputs[3]
+        return mask
+
+    @classmethod
+    def _decode_unmasked(cls, inputs: list[torch.Tensor], attrs: dict) -> bool:
+        """Whether the reference's SDPA leaves a single-query decode row
+        unmasked: no dropout, is_causal unset, and no mask or a positional
+        [.., 1, 1] mask (which its conversion turns into zeros)."""
+        if attrs.get("dropout_p") or attrs.get("is_causal"):
+            return False
+        mask = cls._mask_of(inputs, attrs)
+        if mask is None:
+            return True
+        return bool(mask.dtype.is_floating_point and mask.shape[-1] == 1 and mask.shape[-2] == 1)
+
+    def _decode(self, inputs: list[torch.Tensor], k_slab: str, v_slab: str, layer: int,
+                attrs: dict) -> torch.Tensor | None:
         """q [R, Hq, 1, D] (sorted request order, as the reference's gather)
-        -> [R, Hq, 1, D] over positions [0, max_position], cut to each table."""
+        -> [R, Hq, 1, D] over positions [0, max_position] of every request
+        (`handle` records the op only when each table covers them)."""
         mgr = self.cache_mgr
         tables = self.block_tables
+        q = inputs[0]
         if q.shape[2] != 1 or q.shape[0] != len(tables) or self.positions is None:
             return None
+        if not self._decode_unmasked(inputs, attrs):
+            return None
         seq_len = int(self.positions.max().item()) + 1
-        bs = mgr._block_size
-        lens = [min(seq_len, len(tables[k]) * bs) for k in sorted(tables)]
+        if not self._tables_cover(seq_len):
+            return None
+        lens = [seq_len] * len(tables)
         scale = attrs.get("scale")
         scale = float(scale) if scale is not None else 1.0 / math.sqrt(q.shape[-1])
         out = mgr.attend(q[:, :, 0, :], layer, lens, k_slab=k_slab, v_slab=v_slab, scale=scale)
         return out.unsqueeze(2)
 
-    def _prefill(self, q: torch.Tensor, k_slab: str, v_slab: str, layer: int, attrs: dict) -> torch.Tensor | None:
-        """One request's chunk q [1, Hq, L, D] at this step's positions ->
-        [1, Hq, L, D]: chunked-prefill attention from the slabs."""
+    def _prefill(self, inputs: list[torch.Tensor], k_slab: str, v_slab: str, layer: int,
+                 attrs: dict) -> torch.Tensor | None:
+        """One request's causal chunk q [1, Hq, L, D] at this step's
+        positions -> [1, Hq, L, D]: chunked-prefill attention from the slabs
+        (only with prefill_from_slabs)."""
         mgr = self.cache_mgr
+        q = inputs[0]
         if q.shape[0] != 1 or len(self.block_tables) != 1 or self.positions is None or attrs.get("dropout_p"):
+            return None
+        # causal by position: is_causal, or the reference's positional mask
+        mask = self._mask_of(inputs, attrs)
+        if not (attrs.get("is_causal") or (mask is not None and mask.dtype.is_floating_point)):
             return None
         pos = self.positions.reshape(-1)
         L = q.shape[2]

@@ -5,9 +5,12 @@ The first four tests restate the reference's own intercept cases
 filtering and layer isolation, the exact-not-block-multiple decode gather,
 prefill leaving the SDPA inputs alone) with the reference's policy shape;
 the rest check the outputs that replace the gather + dense SDPA against the
-float64 oracle: decode from the slabs (fp32 and e4m3 slabs) and
-chunked-prefill from the slabs (bf16 queries over e4m3 slabs, a first
-chunk and a later one that also sees the cached prefix).
+float64 oracle and against the reference's own path (gather + dense SDPA):
+decode from the slabs (fp32, bf16 and e4m3 slabs; one request and a
+multi-request batch with mixed table lengths), the default prefill (the
+reference's dense SDPA over the op's own K and V), and the opt-in
+chunked-prefill from the slabs (bf16 queries over e4m3 slabs, a first chunk
+and a later one that also sees the cached prefix).
 """
 
 from __future__ import annotations
@@ -86,7 +89,8 @@ class _DenseSdpa(OpExecutor):
         assert op_name == "scaled_dot_product_attention"
         self.calls += 1
         q, k, v = inputs[0], inputs[1], inputs[2]
-        return F.scaled_dot_product_attention(q.float(), k.float(), v.float(), scale=kwargs.get("scale")).to(q.dtype)
+        return F.scaled_dot_product_attention(q.float(), k.float(), v.float(), scale=kwargs.get("scale"),
+                                              is_causal=bool(kwargs.get("is_causal", False))).to(q.dtype)
 
 
 def test_each_layer_writes_its_own_slab_layer(gpu):
@@ -192,7 +196,8 @@ def test_llama_shaped_prefill_then_decode_from_fp8_slabs(gpu):
     prefix), then a decode at 600 -- every output from the slabs, against the
     float64 oracle on the codes the slabs hold."""
     hq, hkv, d, layers = 32, 8, 128, 2
-    ic = PagedKVIntercept.from_module(_module(layers, heads=hkv, dim=d, dtype="float8_e4m3fn"), device=gpu)
+    ic = PagedKVIntercept.from_module(_module(layers, heads=hkv, dim=d, dtype="float8_e4m3fn"), device=gpu,
+                                      prefill_from_slabs=True)
     for s in ("k", "v"):
         ic.cache_mgr.set_kv_scales(s, torch.full((layers, hkv), 0.02))
     g = torch.Generator(device=gpu).manual_seed(11)
@@ -211,7 +216,8 @@ def test_llama_shaped_prefill_then_decode_from_fp8_slabs(gpu):
             ssa = {f"%k{lay}": k, f"%v{lay}": v}
             ic.handle(_sdpa_op(lay), ssa)
             assert ssa[f"%k{lay}"] is k  # never substituted
-            results.append(ic.run_sdpa(_sdpa_op(lay), [q, k, v], hal))
+            attrs = {} if decode else {"is_causal": True}
+            results.append(ic.run_sdpa(_sdpa_op(lay), [q, k, v], hal, **attrs))
         torch.cuda.synchronize()
         assert hal.calls == 0
         out = results[layer]
@@ -224,3 +230,92 @@ def test_llama_shaped_prefill_then_decode_from_fp8_slabs(gpu):
                                     1 / math.sqrt(d))
         got = out[0].permute(1, 0, 2).float().cpu().numpy()
         assert_close(got, ref, torch.bfloat16, f"intercept llama start={start} n={n}")
+
+
+def test_default_prefill_is_the_reference_dense_sdpa(gpu):
+    """Prefill chunks at 0..255 and 256..511 over e4m3 slabs, bf16
+    activations: by default the op's output is the HAL's dense causal SDPA
+    over the op's own (unquantized) K and V -- the reference's call, bitwise
+    -- and the rows still land in the slabs.  Opting in to prefill from the
+    slabs at position 0 over bf16 slabs gives the same attention within the
+    bf16 tolerance (the slabs hold the op's K and V exactly there)."""
+    hq, hkv, d = 8, 2, 64
+    g = torch.Generator(device=gpu).manual_seed(3)
+    table = list(range(20, 52))  # 32 blocks of the 64-block pool: 512 tokens
+    for dtype, opt_in in (("float8_e4m3fn", False), ("bfloat16", False), ("bfloat16", True)):
+        ic = PagedKVIntercept.from_module(_module(1, heads=hkv, dim=d, dtype=dtype), device=gpu,
+                                          prefill_from_slabs=opt_in)
+        if dtype == "float8_e4m3fn":
+            for s in ("k", "v"):
+                ic.cache_mgr.set_kv_scales(s, torch.full((1, hkv), 0.02))
+        for start in ((0,) if opt_in else (0, 256)):
+            n = 256
+            print(f"[case] default prefill dtype={dtype} opt_in={opt_in} start={start}", flush=True)
+            ic.begin_step({"r0": table}, positions=torch.arange(start, start + n), is_decode=False)
+            q = torch.randn(1, hq, n, d, generator=g, device=gpu).to(torch.bfloat16)
+            k = torch.randn(1, hkv, n, d, generator=g, device=gpu).to(torch.bfloat16)
+            v = torch.randn(1, hkv, n, d, generator=g, device=gpu).to(torch.bfloat16)
+            ssa = {"%k0": k, "%v0": v}
+            ic.handle(_sdpa_op(0), ssa)
+            assert ssa["%k0"] is k and ssa["%v0"] is v
+            hal = _DenseSdpa()
+            kr = k.repeat_interleave(hq // hkv, dim=1)
+            vr = v.repeat_interleave(hq // hkv, dim=1)
+            out = ic.run_sdpa(_sdpa_op(0), [q, kr, vr], hal, is_causal=True)
+            want = _DenseSdpa().execute("scaled_dot_product_attention", [q, kr, vr], is_causal=True)
+            torch.cuda.synchronize()
+            if opt_in:
+                assert hal.calls == 0
+                assert_close(out.float().cpu().numpy(), want.float().cpu().numpy(), torch.bfloat16,
+                             "prefill from bf16 slabs at position 0 vs dense causal SDPA")
+            else:
+                assert hal.calls == 1 and torch.equal(out, want)
+            back = ic.cache_mgr.read_paged("k", 0, start + n)[0, start:start + n].permute(1, 0, 2)
+            if dtype == "bfloat16":
+                assert torch.equal(back.to(torch.bfloat16), k[0]), "rows written to the slab"
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_multi_request_decode_matches_the_reference_gather(gpu, dtype):
+    """Three requests (sorted ids differ from insertion order), GQA 8/2
+    heads, tables of 3, 2 and 4 blocks.  A decode step whose position every
+    table covers is answered from the slabs and equals the reference's path
+    (gather + dense SDPA, replace_inputs=True); a step past the shortest
+    table -- where the reference's gather adds zero rows to that request's
+    softmax -- gathers as the reference does, so both paths agree there
+    too, bitwise."""
+    hq, hkv, d = 8, 2, 64
+    tdt = {"float32": torch.float32, "bfloat16": torch.bfloat16}[dtype]
+    g = torch.Generator(device=gpu).manual_seed(9)
+    tables = {"rb": [7, 3, 11], "ra": [0, 5], "rc": [20, 21, 22, 23]}
+    rows = {rid: torch.randn(len(t) * 16, hkv, d, generator=g, device=gpu).to(tdt) for rid, t in tables.items()}
+    outs = {}
+    for replace in (False, True):
+        ic = PagedKVIntercept.from_module(_module(1, heads=hkv, dim=d, dtype=dtype), device=gpu,
+                                          replace_inputs=replace)
+        for rid, t in tables.items():  # fill every request's blocks through its own table
+            ic.begin_step({rid: t}, positions=torch.arange(len(t) * 16), is_decode=False)
+            kv = rows[rid].permute(1, 0, 2).unsqueeze(0)
+            ic.handle(_sdpa_op(0), {"%k0": kv, "%v0": kv * 0.5})
+        for pos in (20, 40):
+            print(f"[case] multi-request decode dtype={dtype} replace={replace} pos={pos}", flush=True)
+            ic.begin_step(tables, positions=torch.tensor([pos]), is_decode=True)
+            knew = torch.randn(1, hkv, 1, d, generator=torch.Generator(device=gpu).manual_seed(pos),
+                               device=gpu).to(tdt)
+            ssa = {"%k0": knew, "%v0": knew * 0.5}
+            ic.handle(_sdpa_op(0), ssa)
+            q = torch.randn(3, hq, 1, d, generator=torch.Generator(device=gpu).manual_seed(100 + pos),
+                            device=gpu).to(tdt)
+            hal = _DenseSdpa()
+            k_in, v_in = ssa["%k0"], ssa["%v0"]
+            if k_in.shape[1] == hkv and k_in.shape[2] > 1:  # gathered operands: GQA for the dense HAL
+                k_in = k_in.repeat_interleave(hq // hkv, dim=1)
+                v_in = v_in.repeat_interleave(hq // hkv, dim=1)
+            outs[(replace, pos)] = (ic.run_sdpa(_sdpa_op(0), [q, k_in, v_in], hal).float().cpu(), hal.calls)
+    torch.cuda.synchronize()
+    # position 20: every table covers 21 tokens -> kernel vs the reference's dense path
+    assert outs[(False, 20)][1] == 0 and outs[(True, 20)][1] == 1
+    assert_close(outs[(False, 20)][0].numpy(), outs[(True, 20)][0].numpy(), tdt, "multi-request decode")
+    # position 40: "ra" holds 32 tokens -> both gather, zero rows included
+    assert outs[(False, 40)][1] == 1 and outs[(True, 40)][1] == 1
+    assert torch.equal(outs[(False, 40)][0], outs[(True, 40)][0])

@@ -126,13 +126,42 @@ def test_decode_answers_from_the_slabs_and_prefill_goes_to_the_hal():
     assert hal.calls == 1 and out.shape == q.shape
     assert ("attend", "k", "v", 0, [21], 0.25) in mgr.calls
     assert not any(c[0] == "read" for c in mgr.calls)
-    # a length past the table is cut to it (the reference would pad with zero rows)
+    # a position past the table: the reference's gather pads with zero rows
+    # that enter its softmax, so this step gathers and the op runs on the HAL
     ic.begin_step({"r0": [0]}, positions=torch.tensor([20]), is_decode=True)
+    ssa = {"%k0": torch.zeros(1, 2, 1, 4), "%v0": torch.zeros(1, 2, 1, 4)}
+    n_attend = sum(c[0] == "attend" for c in mgr.calls)
+    ic.handle(_op(0), ssa)
+    assert ("read", "k", 0, 21) in mgr.calls and ("read", "v", 0, 21) in mgr.calls
+    assert ssa["%k0"].shape == (1, 2, 21, 4)
+    ic.run_sdpa(_op(0), [q, ssa["%k0"], ssa["%v0"]], hal)
+    assert hal.calls == 2 and sum(c[0] == "attend" for c in mgr.calls) == n_attend
+    # several requests, every table long enough: one attend over all of them
+    ic.begin_step({"r1": [2, 3], "r0": [0, 1]}, positions=torch.tensor([17]), is_decode=True)
     ic.handle(_op(0), {"%k0": torch.zeros(1, 2, 1, 4), "%v0": torch.zeros(1, 2, 1, 4)})
-    ic.run_sdpa(_op(0), [q], hal)
-    assert mgr.calls[-1][:5] == ("attend", "k", "v", 0, [16])
+    ic.run_sdpa(_op(0), [torch.zeros(2, 8, 1, 4)], hal)
+    assert mgr.calls[-1][:5] == ("attend", "k", "v", 0, [18, 18]) and hal.calls == 2
+    # a decode op the reference would mask (is_causal, or a boolean mask):
+    # the reference's gathered operands go to the HAL
+    ic.begin_step({"r0": [0, 1]}, positions=torch.tensor([20]), is_decode=True)
+    ic.handle(_op(0), {"%k0": torch.zeros(1, 2, 1, 4), "%v0": torch.zeros(1, 2, 1, 4)})
+    ic.run_sdpa(_op(0), [q, torch.zeros(1, 2, 1, 4), torch.zeros(1, 2, 1, 4)], hal, is_causal=True)
+    assert hal.calls == 3 and mgr.calls[-1] == ("read", "v", 0, 21)
     # an op no intercept matched runs through the HAL
     ic.run_sdpa(_op(0, "%kx", "%vx"), [q], hal)
+    assert hal.calls == 4
+
+
+def test_prefill_from_slabs_is_opt_in_and_causal_only():
+    mgr = _Mgr()
+    hal = _Hal()
+    for opt_in in (False, True):
+        ic = PagedKVIntercept(mgr, _intercepts(1), _producers(1), prefill_from_slabs=opt_in)
+        ic.begin_step({"r0": [0]}, positions=torch.arange(3), is_decode=False)
+        ic.handle(_op(0), {"%k0": torch.zeros(1, 2, 3, 4), "%v0": torch.zeros(1, 2, 3, 4)})
+        assert bool(ic._pending) == opt_in
+        # fp32 slabs here: even when opted in, the chunk kernel does not apply
+        ic.run_sdpa(_op(0), [torch.zeros(1, 8, 3, 4)], hal, is_causal=True)
     assert hal.calls == 2
 
 

@@ -63,6 +63,49 @@ def test_noalloc_matches_workspace_entry_point(gpu):
         assert torch.equal(out, want), f"call {i}: no-alloc output differs from the workspace entry point"
 
 
+def test_noalloc_allocates_nothing_and_replays_in_a_graph(gpu):
+    """The entry point under HIP graph capture (torch.cuda.graph): captured
+    once, replayed four times with eager work between the replays (other
+    no-alloc and workspace calls over the same scratch and a refill of the
+    output), each replay bitwise equal to the workspace entry point; torch's
+    allocator sees no allocation across an eager call or a replay."""
+    case = workloads.make_case("c3_llama3_8b", device=gpu, seed=5, batch=16)
+    kc, vc, ks, vs = workloads.materialize(case, "paired")
+    sh = torch.tensor(ops.shared_prefix_lens(case.block_tables, case.seq_lens, 16), dtype=torch.int32, device=gpu)
+    args = (case, kc, vc, ks, vs, case.tables_tensor(gpu), case.seq_lens_tensor(gpu), sh)
+    want = _with_workspace(*args)
+    other = workloads.make_case("c2_tinyllama", device=gpu, seed=6, batch=7)
+    okc, ovc, oks, ovs = workloads.materialize(other, "native")
+    oargs = (other, okc, ovc, oks, ovs, other.tables_tensor(gpu), other.seq_lens_tensor(gpu), None)
+    oout = torch.empty(other.q.shape, dtype=other.q.dtype, device=gpu)
+    out = torch.full(case.q.shape, float("nan"), dtype=case.q.dtype, device=gpu)
+    torch.cuda.synchronize()
+    print("[case] no-alloc eager call, allocator counters", flush=True)
+    before = torch.cuda.memory_allocated(gpu)
+    assert _noalloc(*args, out) == 0, _abi.last_error()
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated(gpu) == before
+    assert torch.equal(out, want)
+    print("[case] no-alloc captured in a graph", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _noalloc(*args, out)
+    assert rc == 0, _abi.last_error()
+    torch.cuda.synchronize()
+    for r in range(4):
+        print(f"[case] graph replay {r}", flush=True)
+        out.fill_(float("nan"))
+        assert _noalloc(*oargs, oout) == 0, _abi.last_error()  # leaves other contents in the scratch
+        torch.cuda.synchronize()
+        before = torch.cuda.memory_allocated(gpu)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.cuda.memory_allocated(gpu) == before
+        assert torch.equal(out, want), f"replay {r} differs from the workspace entry point"
+        _with_workspace(*oargs)
+        torch.cuda.synchronize()
+
+
 def test_noalloc_rejects_calls_beyond_its_scratch(gpu):
     """A batch whose workspace exceeds the fixed scratch is refused before any
     launch, with CF_ERR_WORKSPACE and the need in the message."""
