@@ -8,6 +8,12 @@ decode attention call (one layer) over the whole batch; tokens/s = B / step.
 Two copies of the cache pool alternate between steps so the 256 MB
 Infinity Cache does not hold the previous step's KV.
 
+Before the W warm-up steps the GPU is brought to a steady step time
+(`settle`: untimed steps until three timed batches agree; an idle MI355X
+runs its first ~100-200 launches of this workload 10-15 % slower while its
+clocks ramp).  The K timed steps are bracketed by device synchronizations
+and timed with HIP events on the launch stream.
+
 Prints one JSON line (rank 0).  The CPU baseline is the oracle's
 restatement of the reference CPU path (gather + dequantize + SDPA) on a
 bounded sample of the same workload, timed on this host's cores.
@@ -113,6 +119,39 @@ def cpu_share() -> tuple[int, dict]:
                            "omp_num_threads": omp or None}
 
 
+def settle(step, batch: int, max_steps: int, min_steps: int = 0, tol: float = 0.005) -> dict:
+    """Untimed steps until the GPU's step time is steady.
+
+    An idle MI355X runs its first ~100-200 launches of this workload
+    10-15 % slower than it runs them a few tens of ms later (its clocks
+    ramp up under load; measured: 122.5 us per c3 step over the first 20
+    timed steps after 20 warm-up steps, 108.2 us once settled), so a short
+    warm-up alone would time the ramp.  Batches of `batch` steps are timed
+    with HIP events until three in a row agree within `tol` (after at least
+    `min_steps`), at most `max_steps` steps; the W warm-up steps and the
+    timed K steps follow.
+    `step(i)` runs step i.  Returns the batches' per-step times."""
+    import torch
+
+    times: list[float] = []
+    i = 0
+    while i < max_steps:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(batch):
+            step(i)
+            i += 1
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / batch)
+        if (i >= min_steps and len(times) >= 3
+                and all(abs(times[-k] - times[-k - 1]) <= tol * times[-k] for k in (1, 2))):
+            break
+    return {"steps": i, "batch_steps": batch, "us_per_step_by_batch": [round(t * 1e3, 1) for t in times],
+            "rule": f"batches of {batch} untimed steps until three in a row agree within {tol:.1%} "
+                    f"(at least {min_steps}, at most {max_steps} steps), before the W warm-up steps"}
+
+
 def load_traffic(config: str, kernel: str | None = None) -> float | None:
     """Calibrated HBM bytes per launch (FETCH_SIZE / WRITE_SIZE counter
     runs, profiles/traffic_<config>.json) of the config's main kernel, or of
@@ -167,6 +206,11 @@ def bench_mixed(args) -> dict:
     log(f"c5: {alg['decode_tokens']} decodes, {alg['prefill_tokens']} chunk rows; decode bytes "
         f"{alg['decode_bytes'] / 1e9:.2f} GB, prefill {alg['prefill_flops'] / 1e9:.1f} GFLOP")
     one = args.one_stream
+    settled = None
+    if not args.no_settle:
+        settled = settle(lambda i: steps_fns[i % len(steps_fns)](serial=one), batch=5, min_steps=40,
+                         max_steps=150)
+        log(f"settle: {settled['steps']} steps, us/step by batch {settled['us_per_step_by_batch']}")
     for i in range(args.warmup):
         steps_fns[i % len(steps_fns)](serial=one)
     torch.cuda.synchronize()
@@ -223,6 +267,7 @@ def bench_mixed(args) -> dict:
                    "block_size": case.block_size, "kv_layout": args.layout, "cache_pools_rotated": args.pools,
                    "parallelism": "single GPU"},
         "kernel_us": us,
+        "settle": settled,
         "overlap": {"decode_prefill_streams": 1 if one else 2, "ms_per_step_one_stream": ms_serial,
                     "note": "kernel_us are one-stream durations; value is the two-stream step"},
         "algorithmic": alg,
@@ -488,6 +533,8 @@ def main() -> None:
     ap.add_argument("--cpu-sample", type=int, default=8)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-settle", action="store_true",
+                    help="skip the untimed steps that bring the GPU to a steady step time before the warm-up")
     ap.add_argument("--one-stream", action="store_true",
                     help="c5_mixed: decode and prefill one after another only (per-kernel profiles)")
     ap.add_argument("--no-shared-prefix", action="store_true",
@@ -544,6 +591,10 @@ def main() -> None:
     torch.cuda.synchronize()
     log(f"batch {case.batch}, {ab['tokens']} context tokens, unique bytes {ab['unique'] / 1e6:.1f} MB")
 
+    settled = None
+    if not args.no_settle:
+        settled = settle(lambda i: plans[i % len(plans)].run(), batch=20, min_steps=240, max_steps=800)
+        log(f"settle: {settled['steps']} steps, us/step by batch {settled['us_per_step_by_batch']}")
     for i in range(args.warmup):
         plans[i % len(plans)].run()
     torch.cuda.synchronize()
@@ -698,6 +749,7 @@ def main() -> None:
             "shared_prefix_statement": shared is not None,
             "parallelism": "single GPU",
         },
+        "settle": settled,
         "ms_per_step_wall_clock": ms_step_wall,
         "ms_per_step_stamped_launches": ms_step_stamped,
         "step_timing": "ms_per_step = HIP events on the launch stream around the K steps (GPU interval); "
