@@ -191,17 +191,19 @@ int32_t cf_prefill_chunk_workspace_bytes(int64_t num_q_tokens, int64_t num_chunk
  * is cached.  The chunk's own K/V are in the cache already
  * (cf_kv_write_fp8).
  *
- *   q            [Tq, Hq, D]           bf16, D stride 1, rows of all chunks
- *   k_cache,     [NB, 16, Hkv, D]      bf16 | e4m3fn, native or paired tiles,
- *   v_cache                            or the reference's token-major rows
- *                                      (16-byte aligned token rows)
+ *   q            [Tq, Hq, D]           bf16 | f16, D stride 1, rows of all
+ *                                      chunks
+ *   k_cache,     [NB, 16, Hkv, D]      bf16 | f16 | e4m3fn (bf16 q: bf16 or
+ *   v_cache                            e4m3fn; f16 q: f16 or e4m3fn), native
+ *                                      or paired tiles, or the reference's
+ *                                      token-major rows (16-byte aligned)
  *   block_tables [N, Mb]               i32, one row per chunk's sequence
  *   seq_lens     [N]                   i32, tokens of the sequence including
  *                                      the chunk
  *   q_start      [N + 1]               i32, chunk n owns q rows
  *                                      [q_start[n], q_start[n+1])
  *   k_scale, v_scale                   as cf_paged_decode
- *   out          [Tq, Hq, D]           bf16
+ *   out          [Tq, Hq, D]           q's dtype
  *
  * Chunk n has L = q_start[n+1] - q_start[n] rows; row i sits at position
  * seq_lens[n] - L + i and attends to cache positions [0, that] (causal:

@@ -233,13 +233,14 @@ def prefill_chunk(
 ) -> torch.Tensor:
     """Chunked-prefill attention over the paged cache; returns out [Tq, Hq, D].
 
-    q [Tq, Hq, D] bf16 holds the rows of N chunks, chunk n owning rows
-    [q_start[n], q_start[n+1]); block_tables int32 [N, Mb]; seq_lens int32
-    [N] counts the sequence's tokens including the chunk (already written
-    to the cache).  Row i of a chunk of L rows attends causally to cache
-    positions [0, seq_lens[n] - L + i].  Caches: bf16 or e4m3fn, block_size
-    16, in the native or paired tile layout or the reference's token-major
-    rows ([NB, 16, Hkv, D] contiguous).
+    q [Tq, Hq, D] bf16 or fp16 holds the rows of N chunks, chunk n owning
+    rows [q_start[n], q_start[n+1]); block_tables int32 [N, Mb]; seq_lens
+    int32 [N] counts the sequence's tokens including the chunk (already
+    written to the cache).  Row i of a chunk of L rows attends causally to
+    cache positions [0, seq_lens[n] - L + i].  Caches: bf16 or e4m3fn under
+    bf16 q, fp16 or e4m3fn under fp16 q, block_size 16, in the native or
+    paired tile layout or the reference's token-major rows ([NB, 16, Hkv,
+    D] contiguous).
     """
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("block_tables", block_tables),
                     ("seq_lens", seq_lens), ("q_start", q_start)):

@@ -485,15 +485,16 @@ int32_t cf_prefill_chunk_fp8(const CfTensor* q, const CfTensor* k_cache, const C
   if ((rc = view_of(q_start, "q_start", 1, &vqs))) return rc;
   if ((rc = view_of(out, "out", 3, &vo))) return rc;
 
-  CF_CHECK(vq.dtype == CF_BF16, "q: dtype must be bf16, got %s", dtype_name(vq.dtype));
-  CF_CHECK(vk.dtype == CF_BF16 || vk.dtype == CF_F8E4M3FN, "k_cache: dtype must be bf16 or f8e4m3fn, got %s",
-           dtype_name(vk.dtype));
+  CF_CHECK(vq.dtype == CF_BF16 || vq.dtype == CF_F16, "q: dtype must be bf16 or f16, got %s", dtype_name(vq.dtype));
+  CF_CHECK(vk.dtype == CF_BF16 || vk.dtype == CF_F16 || vk.dtype == CF_F8E4M3FN,
+           "k_cache: dtype must be bf16, f16 or f8e4m3fn, got %s", dtype_name(vk.dtype));
   CF_CHECK(vv.dtype == vk.dtype, "v_cache dtype %s differs from k_cache dtype %s", dtype_name(vv.dtype),
            dtype_name(vk.dtype));
   CF_CHECK(vt.dtype == CF_I32, "block_tables: expected i32, got %s", dtype_name(vt.dtype));
   CF_CHECK(vs.dtype == CF_I32, "seq_lens: expected i32, got %s", dtype_name(vs.dtype));
   CF_CHECK(vqs.dtype == CF_I32, "q_start: expected i32, got %s", dtype_name(vqs.dtype));
-  CF_CHECK(vo.dtype == CF_BF16, "out: dtype must be bf16, got %s", dtype_name(vo.dtype));
+  CF_CHECK(vo.dtype == vq.dtype, "out: dtype %s differs from q dtype %s", dtype_name(vo.dtype),
+           dtype_name(vq.dtype));
 
   const int64_t Tq = vq.size[0], Hq = vq.size[1], D = vq.size[2];
   const int64_t NB = vk.size[0], bs = vk.size[1], Hkv = vk.size[2];
@@ -557,8 +558,9 @@ int32_t cf_prefill_chunk_fp8(const CfTensor* q, const CfTensor* k_cache, const C
     CF_CHECK(k_scale == nullptr && v_scale == nullptr, "k_scale/v_scale apply to f8e4m3fn caches only");
   }
   if (!prefill_supported(p, vq.dtype, vk.dtype)) {
-    set_error("prefill: needs head_dim 64/128, GQA group 1/2/4/8/16, native or token-major caches with "
-              "16-byte aligned blocks, heads and token rows, and 16-byte aligned q rows");
+    set_error("prefill: needs bf16 q over bf16/e4m3 caches or f16 q over f16/e4m3 caches, head_dim 64/128, "
+              "GQA group 1/2/4/8/16, native or token-major caches with 16-byte aligned blocks, heads and token "
+              "rows, and 16-byte aligned q rows");
     return CF_ERR_UNSUPPORTED;
   }
   if (Tq == 0 || N == 0) return CF_OK;
@@ -573,7 +575,7 @@ int32_t cf_prefill_chunk_fp8(const CfTensor* q, const CfTensor* k_cache, const C
   }
   CF_CHECK(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
   prefill_bind_workspace(p, workspace);
-  return launch_prefill(p, vk.dtype, as_stream(stream));
+  return launch_prefill(p, vq.dtype, vk.dtype, as_stream(stream));
 }
 
 int32_t cf_fp8_amax_scale(const CfTensor* x, CfTensor* scales, void* stream) {

@@ -1,4 +1,5 @@
-// Chunked prefill over the paged KV cache (bf16 / e4m3fn; native, paired or token-major).
+// Chunked prefill over the paged KV cache (bf16 queries over bf16 / e4m3fn caches, fp16 queries over
+// fp16 / e4m3fn caches; native, paired or token-major).
 //
 // A chunk of L new query rows whose sequence now holds S tokens (its own
 // K/V already written to the cache) puts row i at position S - L + i; the
@@ -331,7 +332,7 @@ __device__ __forceinline__ uint32_t vtok_keep_mask(int ok, int X, int r, int val
 // V tokens at or past `valid` (tile-relative) or in an invalid block become
 // zero (cache slots there may hold any bits, NaN codes included).
 // FULL: the caller knows every token of the tile is valid.
-template <int KT, int D, bool VTOK, bool FULL = false>
+template <int QT, int KT, int D, bool VTOK, bool FULL = false>
 __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const uint4* vr, const TileIds& t,
                                             int valid, int tid) {
   using Gm = Geo<KT, D>;
@@ -341,7 +342,11 @@ __device__ __forceinline__ void stage_write(uint4* lds, const uint4* kr, const u
     if (Gm::KU % 256 == 0 || u < Gm::KU) {
       const KPiece q = k_piece<KT, D>(u);
       const int s = q.s, cp = q.cp, lane = q.li + 16 * q.lq;
-      if constexpr (KT == kE4M3) {
+      if constexpr (KT == kE4M3 && QT == kF16) {
+        // e4m3 K converts exactly to the fp16 operands fp16 queries multiply
+        lds[(s * Gm::NC + 2 * cp) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_f16(kr[i].x, kr[i].y));
+        lds[(s * Gm::NC + 2 * cp + 1) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_f16(kr[i].z, kr[i].w));
+      } else if constexpr (KT == kE4M3) {
         lds[(s * Gm::NC + 2 * cp) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_bf16(kr[i].x, kr[i].y));
         lds[(s * Gm::NC + 2 * cp + 1) * 64 + lane] = __builtin_bit_cast(uint4, e4m3x8_to_bf16(kr[i].z, kr[i].w));
       } else {
@@ -445,7 +450,7 @@ __device__ __forceinline__ void mask_staged_v(uint4* vr, const TileIds& t, int v
   }
 }
 
-template <int KT, int D, int G, bool VTOK>
+template <int QT, int KT, int D, int G, bool VTOK>
 __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, const int32_t* __restrict__ tables,
                                                               const int4* __restrict__ items,
                                                               const int4* __restrict__ chunks, int* header,
@@ -497,7 +502,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     const int kvlen = uniform(max(0, min(pos0 + rows, cap)));
 
     // This wave's columns: tile k, column li -> item column 32 wave + 16 k + li.
-    bf16x8_t qop[2][NC];
+    QOp<QT> qop[2][NC];
     int lim[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -509,7 +514,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(row0 + rr) * p.q_sr +
                              (int64_t)(h * G + g) * p.q_sh + lq * (D / 4);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) qop[k][c] = as_bf16x8(*(const uint4*)(qrow + 8 * c));
+      for (int c = 0; c < NC; ++c) qop[k][c] = as_qop<QT>(*(const uint4*)(qrow + 8 * c));
     }
     // tokens every column of this wave may see
     int lmin = min(lim[0], lim[1]);
@@ -520,7 +525,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     float qk_scale = p.scale * (kscale ? kscale[h * p.ks_s] : 1.0f) * kLog2e;
     if (qk_scale < 0.0f) {
       // the softmax takes its max on raw scores: keep the scale positive by
-      // negating q instead (exact in bf16)
+      // negating q instead (exact: a sign bit flip in bf16 or fp16)
       qk_scale = -qk_scale;
 #pragma unroll
       for (int k = 0; k < 2; ++k)
@@ -531,7 +536,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
           u.y ^= 0x80008000u;
           u.z ^= 0x80008000u;
           u.w ^= 0x80008000u;
-          qop[k][c] = as_bf16x8(u);
+          qop[k][c] = as_qop<QT>(u);
         }
     }
     // A zero scale makes every score 0 (uniform weights over the visible
@@ -566,25 +571,28 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     TileIds id2 = nt > 2 ? tile_ids(p, trow, 2, kvlen) : id1;
     if (nt > 0) {
       stage_load<KT, D, VTOK>(kr, vr, p, id0, h, tid);
-      stage_write<KT, D, VTOK>(lds[0], kr, vr, id0, kvlen, tid);
+      stage_write<QT, KT, D, VTOK>(lds[0], kr, vr, id0, kvlen, tid);
     }
     if (nt > 1) stage_load<KT, D, VTOK>(kr, vr, p, id1, h, tid);
     __syncthreads();
 
-    using POp = typename std::conditional<KT == kE4M3, f16x8_t, bf16x8_t>::type;
+    // P in fp16 against fp16 V operands (e4m3 V converts exactly; fp16 V as
+    // is); against bf16 V as bf16 hi + lo
+    using POp = typename std::conditional<KT == kBF16, bf16x8_t, f16x8_t>::type;
+    using KOp = QOp<QT>;
 
     // The tile's math per column tile k, in pieces the step below orders so
     // that each batch of MFMAs has independent VALU work beside it.
     // Scores: lane (li, lq) holds s1[v] -> token tok0 + v, s2[v] -> token
     // tok0 + 4 + v.
-    auto qk = [&](auto kc, const bf16x8_t* a1, const bf16x8_t* a2, f32x4_t& s1, f32x4_t& s2) {
+    auto qk = [&](auto kc, const KOp* a1, const KOp* a2, f32x4_t& s1, f32x4_t& s2) {
       constexpr int k = decltype(kc)::value;
       s1 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       s2 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[c], qop[k][c], s1, 0, 0, 0);
-        s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[c], qop[k][c], s2, 0, 0, 0);
+        s1 = mfma16(a1[c], qop[k][c], s1);
+        s2 = mfma16(a2[c], qop[k][c], s2);
       }
     };
     // Scores column tile k may not see (edge tiles only) become -inf, in
@@ -637,7 +645,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       for (int v = 0; v < 8; ++v) {
         const float sv = v < 4 ? s1[v] : s2[v - 4];
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sv, qk_scale, -mref));
-        if constexpr (KT == kE4M3) {
+        if constexpr (KT != kBF16) {
           pk[v] = (_Float16)pv;
         } else {
           const __bf16 hi = (__bf16)pv;
@@ -650,7 +658,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
     // pipe as O[column][0] against a V tile whose channel 0 is all ones.
     auto pv = [&](auto kc, const uint4* vraw, const POp& pk, const POp& pl) {
       constexpr int k = decltype(kc)::value;
-      if constexpr (KT == kE4M3) {
+      if constexpr (KT != kBF16) {
         const _Float16 one = li == 0 ? (_Float16)1.0f : (_Float16)0.0f;
         const f16x8_t ones = {one, one, one, one, one, one, one, one};
         ol[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pk, ol[k], 0, 0, 0);
@@ -671,7 +679,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       }
     };
     // MFMAs of one column tile's P.V (or QK^T) product per batch below.
-    constexpr int kPvMfma = KT == kE4M3 ? NV + 1 : 2 * NV + 2;
+    constexpr int kPvMfma = KT != kBF16 ? NV + 1 : 2 * NV + 2;
     constexpr int kQkMfma = 2 * NC;
 
     // One step: the next tile's registers go to the other LDS buffer and
@@ -694,12 +702,12 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       tp += 2 * tsm;
       const uint4* kl = lds[P];
       const uint4* vl = kl + Gm::KENT;
-      bf16x8_t a1[NC], a2[NC];
+      KOp a1[NC], a2[NC];
       uint4 vraw[NV];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        a1[c] = as_bf16x8(kl[c * 64 + lane]);
-        a2[c] = as_bf16x8(kl[(NC + c) * 64 + lane]);
+        a1[c] = as_qop<QT>(kl[c * 64 + lane]);
+        a2[c] = as_qop<QT>(kl[(NC + c) * 64 + lane]);
       }
       const bool edge = j >= lmin_t || id0.ok != 3;
       const int tok0 = 32 * j + 8 * lq;
@@ -709,7 +717,7 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
       POp pa, pla, pb, plb;
       // QK^T of column tile 0 beside the next tile's conversion into LDS
       qk(K0, a1, a2, s1a, s2a);
-      stage_write<KT, D, VTOK, true>(lds[1 - P], kr, vr, id1, valid_next, tid);
+      stage_write<QT, KT, D, VTOK, true>(lds[1 - P], kr, vr, id1, valid_next, tid);
       stage_load<KT, D, VTOK>(kr, vr, p, id2, h, tid);
       __builtin_amdgcn_sched_group_barrier(0x100, 2 * NC, 0);
 #pragma unroll
@@ -780,10 +788,8 @@ __global__ __launch_bounds__(256, 2) void prefill_item_kernel(PrefillParams p, c
 #pragma unroll
         for (int t = 0; t < NV; ++t) {
           uint2 packed;
-          packed.x = (uint32_t)bf16_bits_from_f32(o[k][t][0] * inv) |
-                     ((uint32_t)bf16_bits_from_f32(o[k][t][1] * inv) << 16);
-          packed.y = (uint32_t)bf16_bits_from_f32(o[k][t][2] * inv) |
-                     ((uint32_t)bf16_bits_from_f32(o[k][t][3] * inv) << 16);
+          packed.x = (uint32_t)out_bits<QT>(o[k][t][0] * inv) | ((uint32_t)out_bits<QT>(o[k][t][1] * inv) << 16);
+          packed.y = (uint32_t)out_bits<QT>(o[k][t][2] * inv) | ((uint32_t)out_bits<QT>(o[k][t][3] * inv) << 16);
           *(uint2*)(orow + 16 * t) = packed;
         }
       }
@@ -800,12 +806,13 @@ int prefill_cus() {
 
 constexpr int kItemBlocksPerCU = 2;  // resident workgroups per CU (8 waves)
 
-template <int KT, int D, int G, bool VTOK>
+template <int QT, int KT, int D, int G, bool VTOK>
 int32_t launch_t(PrefillParams& p, hipStream_t stream) {
   static int per_cu = 0;
   if (per_cu == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_item_kernel<KT, D, G, VTOK>, 256, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_item_kernel<QT, KT, D, G, VTOK>, 256, 0) !=
+            hipSuccess ||
         n < 1)
       n = 1;
     per_cu = n < kItemBlocksPerCU ? n : kItemBlocksPerCU;
@@ -817,30 +824,38 @@ int32_t launch_t(PrefillParams& p, hipStream_t stream) {
   CF_HIP_CHECK(hipGetLastError());
   {
     ProfileScope prof("cf_prefill_mfma", stream);
-    CF_LAUNCH((prefill_item_kernel<KT, D, G, VTOK>), dim3(prefill_cus() * per_cu), dim3(256), 0, stream, p,
+    CF_LAUNCH((prefill_item_kernel<QT, KT, D, G, VTOK>), dim3(prefill_cus() * per_cu), dim3(256), 0, stream, p,
                        p.tables, (const int4*)p.items, (const int4*)p.chunks, p.header, p.k_scale, p.v_scale);
   }
   CF_HIP_CHECK(hipGetLastError());
   return CF_OK;
 }
 
-template <int KT, int D, bool VTOK>
+template <int QT, int KT, int D, bool VTOK>
 int32_t launch_v(PrefillParams& p, hipStream_t stream) {
   switch (p.G) {
-    case 1: return launch_t<KT, D, 1, VTOK>(p, stream);
-    case 2: return launch_t<KT, D, 2, VTOK>(p, stream);
-    case 4: return launch_t<KT, D, 4, VTOK>(p, stream);
-    case 8: return launch_t<KT, D, 8, VTOK>(p, stream);
-    case 16: return launch_t<KT, D, 16, VTOK>(p, stream);
+    case 1: return launch_t<QT, KT, D, 1, VTOK>(p, stream);
+    case 2: return launch_t<QT, KT, D, 2, VTOK>(p, stream);
+    case 4: return launch_t<QT, KT, D, 4, VTOK>(p, stream);
+    case 8: return launch_t<QT, KT, D, 8, VTOK>(p, stream);
+    case 16: return launch_t<QT, KT, D, 16, VTOK>(p, stream);
   }
   set_error("prefill: unsupported GQA group %d", p.G);
   return CF_ERR_UNSUPPORTED;
 }
 
 // V in token rows (token stride != 1) or the native channel rows
-template <int KT, int D>
+template <int QT, int KT, int D>
 int32_t launch_g(PrefillParams& p, hipStream_t stream) {
-  return p.v_s[1] != 1 ? launch_v<KT, D, true>(p, stream) : launch_v<KT, D, false>(p, stream);
+  return p.v_s[1] != 1 ? launch_v<QT, KT, D, true>(p, stream) : launch_v<QT, KT, D, false>(p, stream);
+}
+
+template <int QT, int KT>
+int32_t launch_d(PrefillParams& p, hipStream_t stream) {
+  if (p.D == 128) return launch_g<QT, KT, 128>(p, stream);
+  if (p.D == 64) return launch_g<QT, KT, 64>(p, stream);
+  set_error("prefill: unsupported head_dim %d", p.D);
+  return CF_ERR_UNSUPPORTED;
 }
 
 uint64_t pad256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
@@ -848,8 +863,14 @@ uint64_t pad256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
 }  // namespace
 
 bool prefill_supported(const PrefillParams& p, int q_dt, int kv_dt) {
-  if (q_dt != kBF16) return false;
-  if (kv_dt != kBF16 && kv_dt != kE4M3) return false;
+  // bf16 queries over bf16 or e4m3 caches; fp16 queries over fp16 or e4m3
+  if (q_dt == kBF16) {
+    if (kv_dt != kBF16 && kv_dt != kE4M3) return false;
+  } else if (q_dt == kF16) {
+    if (kv_dt != kF16 && kv_dt != kE4M3) return false;
+  } else {
+    return false;
+  }
   if (p.D != 64 && p.D != 128) return false;
   if (p.G != 1 && p.G != 2 && p.G != 4 && p.G != 8 && p.G != 16) return false;
   if (p.NB < 1) return false;
@@ -890,16 +911,9 @@ void prefill_bind_workspace(PrefillParams& p, void* workspace) {
   p.header = (int*)w;
 }
 
-int32_t launch_prefill(PrefillParams& p, int kv_dt, hipStream_t stream) {
-  if (kv_dt == kE4M3) {
-    if (p.D == 128) return launch_g<kE4M3, 128>(p, stream);
-    if (p.D == 64) return launch_g<kE4M3, 64>(p, stream);
-  } else {
-    if (p.D == 128) return launch_g<kBF16, 128>(p, stream);
-    if (p.D == 64) return launch_g<kBF16, 64>(p, stream);
-  }
-  set_error("prefill: unsupported head_dim %d", p.D);
-  return CF_ERR_UNSUPPORTED;
+int32_t launch_prefill(PrefillParams& p, int q_dt, int kv_dt, hipStream_t stream) {
+  if (q_dt == kF16) return kv_dt == kE4M3 ? launch_d<kF16, kE4M3>(p, stream) : launch_d<kF16, kF16>(p, stream);
+  return kv_dt == kE4M3 ? launch_d<kBF16, kE4M3>(p, stream) : launch_d<kBF16, kBF16>(p, stream);
 }
 
 }  // namespace cf

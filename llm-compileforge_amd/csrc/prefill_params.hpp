@@ -39,6 +39,6 @@ int prefill_rows_per_item(int G);
 bool prefill_supported(const PrefillParams& p, int q_dt, int kv_dt);
 uint64_t prefill_workspace_bytes(int64_t Tq, int64_t N, int64_t Hq, int64_t Hkv, int64_t D);
 void prefill_bind_workspace(PrefillParams& p, void* workspace);
-int32_t launch_prefill(PrefillParams& p, int kv_dt, hipStream_t stream);
+int32_t launch_prefill(PrefillParams& p, int q_dt, int kv_dt, hipStream_t stream);
 
 }  // namespace cf

@@ -288,11 +288,12 @@ def chunked_prefill_attention(
     """Attention of prefill chunks over the paged cache.
 
     Args:
-        q: [Tq, Hq, D] bf16, the query rows of all chunks.
-        k_cache, v_cache: [num_blocks, 16, Hkv, D] bf16 or float8_e4m3fn in
-            any layout of cf_hip.layout.alloc_kv_cache (the reference's
-            token-major one included); the chunk's own K/V must already be
-            written.
+        q: [Tq, Hq, D] bf16 or float16, the query rows of all chunks.
+        k_cache, v_cache: [num_blocks, 16, Hkv, D] in any layout of
+            cf_hip.layout.alloc_kv_cache (the reference's token-major one
+            included): bfloat16 or float8_e4m3fn under bf16 queries,
+            float16 or float8_e4m3fn under float16 queries; the chunk's own
+            K/V must already be written.
         block_tables: int32 [N, Mb], one row per chunk's sequence.
         seq_lens: int32 [N], tokens of each sequence including its chunk.
         q_start: int32 [N + 1]; chunk n owns q rows [q_start[n], q_start[n+1]).
@@ -305,7 +306,7 @@ def chunked_prefill_attention(
     kernels/flash_attention.py:179-202).
 
     Returns:
-        [Tq, Hq, D] bf16.
+        [Tq, Hq, D] in q's dtype.
     """
     _require_rocm(q)
     if scale is None:

@@ -28,7 +28,8 @@ path:
   - prefill: the SDPA inputs stay untouched and the op runs on the HAL, as
     in the reference (dense attention over the op's own K and V with its
     positional mask).  With prefill_from_slabs=True, a single request's
-    causal chunk with bf16 queries over bf16 / e4m3 slabs runs
+    causal chunk with bf16 queries over bf16 / e4m3 slabs (or fp16 queries
+    over fp16 / e4m3 slabs) runs
     chunked-prefill attention from the slabs instead (CacheManager
     .attend_chunks: the row at position p sees positions [0, p]).  That is
     a different operation, not a faster route to the same one: it reads K
@@ -302,7 +303,9 @@ class PagedKVIntercept:
         if pos.numel() != L or L == 0:
             return None
         kv, vv = mgr.layer_view(k_slab, layer), mgr.layer_view(v_slab, layer)
-        if q.dtype != torch.bfloat16 or kv.dtype not in (torch.bfloat16, torch.float8_e4m3fn) or mgr._block_size != 16:
+        kernel_dtypes = {torch.bfloat16: (torch.bfloat16, torch.float8_e4m3fn),
+                         torch.float16: (torch.float16, torch.float8_e4m3fn)}
+        if kv.dtype not in kernel_dtypes.get(q.dtype, ()) or mgr._block_size != 16:
             return None
         p0 = int(pos[0].item())
         if not bool(torch.equal(pos.cpu(), torch.arange(p0, p0 + L))):

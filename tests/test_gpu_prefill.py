@@ -91,6 +91,37 @@ def test_shapes_match_oracle(gpu, hq, hkv, d, kv_dtype, layout):
     assert_close(out.float().cpu().numpy(), ref, torch.bfloat16, f"prefill {hq}/{hkv}/{d}/{kv_dtype}")
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 1, 128), (32, 2, 64)])
+@pytest.mark.parametrize("kv_dtype", [torch.float16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("layout", ["paired", "token_major"])
+def test_fp16_queries_match_oracle(gpu, hq, hkv, d, kv_dtype, layout):
+    """fp16 queries (an fp16 model's prefill) over fp16 or e4m3 caches: the
+    kernel's fp16 operand path (e4m3 K and V convert exactly to fp16) against
+    the float64 oracle on the same fp16 queries, fp16 output."""
+    print(f"[case] fp16-q prefill hq={hq} hkv={hkv} d={d} kv={kv_dtype} layout={layout}", flush=True)
+    case = workloads.make_mixed_case(device=gpu, seed=3 * hq + d, chunks=[1, 17, 64, 100, 33],
+                                     cached=[0, 5, 300, 33, 1000], decode_lens=[], num_q_heads=hq,
+                                     num_kv_heads=hkv, head_dim=d, kv_dtype=kv_dtype)
+    t = workloads.materialize_mixed(case, layout)
+    _write_new_rows(case, t)
+    q16 = t["q_prefill"].to(torch.float16)
+    out = _prefill(case, t, q=q16)
+    assert out.dtype == torch.float16
+    ref, covered = oracle_prefill(case, t, q=q16)
+    assert covered.all()
+    assert_close(out.float().cpu().numpy(), ref, torch.float16, f"fp16-q prefill {hq}/{hkv}/{d}/{kv_dtype}")
+
+
+def test_fp16_queries_reject_bf16_caches(gpu):
+    """fp16 queries over a bf16 cache have no exact common MFMA operand type:
+    refused (NotImplementedError), as the decode kernel refuses them."""
+    case = workloads.make_mixed_case(device=gpu, seed=21, chunks=[8], cached=[0], decode_lens=[],
+                                     num_q_heads=8, num_kv_heads=2, head_dim=64, kv_dtype=torch.bfloat16)
+    t = workloads.materialize_mixed(case)
+    with pytest.raises(NotImplementedError):
+        _prefill(case, t, q=t["q_prefill"].to(torch.float16))
+
+
 @pytest.mark.parametrize("seed", range(12))
 def test_random_configurations(gpu, seed):
     """Seeded random steps over every supported head shape, cache dtype and
