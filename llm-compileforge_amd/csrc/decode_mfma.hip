@@ -342,11 +342,49 @@ __device__ __forceinline__ Coord advance(const DecodeParams& p, const Index& ix,
   return c;
 }
 
+// Q operand terms per channel: fp32 queries are split exactly into three
+// bf16 terms (hi + mid + lo, 8 significant bits each), 16-bit queries are
+// their own single term.
+template <int QT>
+constexpr int q_terms() {
+  return QT == kF32 ? 3 : 1;
+}
+
 // Q operand columns: column i < ncols is query head (i % G) of KV head h for
-// sequence b + i / G; the rest are zero.
+// sequence b + i / G; the rest are zero.  Term s of channel chunk cc is
+// qop[s * D / 32 + cc].
 template <int QT, int D>
 __device__ __forceinline__ void load_q(QOp<QT>* qop, const DecodeParams& p, const Coord& c, int li, int lq) {
   constexpr int NC = D / 32;
+  if constexpr (QT == kF32) {
+    // x - hi and (x - hi) - mid are exact in fp32, so hi + mid + lo == x
+    // (bf16 has fp32's exponent range).  Unused columns read column 0's row
+    // and keep zeros (no divergent branch around the operand registers).
+    const bool used = li < c.ncols;
+    const int m = used ? li / p.G : 0, g = used ? li - m * p.G : 0;
+    const float* qrow = (const float*)p.q + (int64_t)(c.b + m) * p.q_sb + (int64_t)(c.h * p.G + g) * p.q_sh +
+                        lq * (D / 4);
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const float4 a = *(const float4*)(qrow + 8 * cc), b = *(const float4*)(qrow + 8 * cc + 4);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      bf16x8_t hi, mid, lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xv = used ? x[e] : 0.0f;
+        const __bf16 h = (__bf16)xv;
+        const float r = xv - (float)h;
+        const __bf16 md = (__bf16)r;
+        hi[e] = h;
+        mid[e] = md;
+        lo[e] = (__bf16)(r - (float)md);
+      }
+      qop[cc] = hi;
+      qop[NC + cc] = mid;
+      qop[2 * NC + cc] = lo;
+    }
+    return;
+  }
   if (li < c.ncols) {
     const int m = li / p.G, g = li - m * p.G;
     const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(c.b + m) * p.q_sb + (int64_t)(c.h * p.G + g) * p.q_sh +
@@ -356,6 +394,26 @@ __device__ __forceinline__ void load_q(QOp<QT>* qop, const DecodeParams& p, cons
   } else {
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) qop[cc] = as_qop<QT>(make_uint4(0, 0, 0, 0));
+  }
+}
+
+// Outputs: bf16 / fp16 codes for 16-bit queries, fp32 for fp32 queries.
+template <int QT>
+__device__ __forceinline__ void store_out1(void* out, int64_t off, float v) {
+  if constexpr (QT == kF32) ((float*)out)[off] = v;
+  else ((uint16_t*)out)[off] = out_bits<QT>(v);
+}
+
+// Four consecutive outputs (8-byte aligned codes, 16-byte aligned fp32).
+template <int QT>
+__device__ __forceinline__ void store_out4(void* out, int64_t off, float a, float b, float c, float d) {
+  if constexpr (QT == kF32) {
+    *(float4*)((float*)out + off) = make_float4(a, b, c, d);
+  } else {
+    uint2 packed;
+    packed.x = (uint32_t)out_bits<QT>(a) | ((uint32_t)out_bits<QT>(b) << 16);
+    packed.y = (uint32_t)out_bits<QT>(c) | ((uint32_t)out_bits<QT>(d) << 16);
+    *(uint2*)((uint16_t*)out + off) = packed;
   }
 }
 
@@ -406,14 +464,10 @@ __device__ __forceinline__ void flush_run(const DecodeParams& p, const Index& ix
   if (li >= c.ncols) return;
   if (direct) {
     const float inv = lt > 0.0f ? vs / lt : 0.0f;
-    uint16_t* orow = (uint16_t*)p.out + (int64_t)c.b * p.o_sb + (int64_t)(c.h * G + li) * p.o_sh + 4 * lq;
+    const int64_t orow = (int64_t)c.b * p.o_sb + (int64_t)(c.h * G + li) * p.o_sh + 4 * lq;
 #pragma unroll
-    for (int t = 0; t < NV; ++t) {
-      uint2 packed;
-      packed.x = (uint32_t)out_bits<QT>(o[t][0] * inv) | ((uint32_t)out_bits<QT>(o[t][1] * inv) << 16);
-      packed.y = (uint32_t)out_bits<QT>(o[t][2] * inv) | ((uint32_t)out_bits<QT>(o[t][3] * inv) << 16);
-      *(uint2*)(orow + 16 * t) = packed;
-    }
+    for (int t = 0; t < NV; ++t)
+      store_out4<QT>(p.out, orow + 16 * t, o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
     return;
   }
   int64_t row;
@@ -486,8 +540,8 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   // visited); wave w takes sequences w, w + Wtot, ...
   for (int bz = w; bz < p.B; bz += Wtot) {
     if (eff_len(p, ix, bz) == 0) {
-      uint16_t* orow = (uint16_t*)p.out + (int64_t)bz * p.o_sb;
-      for (int e = lane; e < p.Hq * D; e += 64) orow[(int64_t)(e / D) * p.o_sh + e % D] = 0;
+      const int64_t orow = (int64_t)bz * p.o_sb;
+      for (int e = lane; e < p.Hq * D; e += 64) store_out1<QT>(p.out, orow + (int64_t)(e / D) * p.o_sh + e % D, 0.0f);
       for (int hh = lane; hh < p.Hkv; hh += 64) {
         p.own_desc[(int64_t)bz * p.Hkv + hh] = make_int2(0, 0);
         p.pre_desc[(int64_t)bz * p.Hkv + hh] = make_int2(0, 0);
@@ -543,7 +597,8 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   TileRegs<KT, D, VTOK> r0, r1;
   load_tile<KT, D, VTOK>(r0, kv, c0.blkA, c0.blkB, li, lq, c0.h, lane);
 
-  QOp<QT> qop[NC];
+  constexpr int QS = q_terms<QT>();
+  QOp<QT> qop[QS * NC];
   load_q<QT, D>(qop, p, c0, li, lq);
   float m = -INFINITY, l = 0.0f;
   f32x4_t o[NV];
@@ -552,13 +607,17 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
   int run_j0 = c0.j;
   bool first_run = true;
 
-  QOp<QT> qnext[NC];  // the next run's q columns, loaded a tile ahead
+  // the next run's q columns, loaded a tile ahead (fp32 queries load theirs
+  // when the run starts: three terms a tile ahead would not fit the registers)
+  QOp<QT> qnext[QT == kF32 ? 1 : NC];
   for (;;) {
     // A run ends with this tile: the next run's q loads go out now, ahead
     // of the next tile's K/V, so they have landed when that tile computes
     // (a load issued after the flush would stall it a full round trip).
     const bool run_ends = !has1 || c1.b != c0.b || c1.h != c0.h || c1.kind != c0.kind;
-    if (has1 && run_ends) load_q<QT, D>(qnext, p, c1, li, lq);
+    if constexpr (QT != kF32) {
+      if (has1 && run_ends) load_q<QT, D>(qnext, p, c1, li, lq);
+    }
     // Always issue the next tile's loads (the last iteration reloads its
     // own tile) so every path has the same number of loads in flight and
     // the compiler's vmcnt waits stay exact.
@@ -573,8 +632,19 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     f32x4_t s1 = {0.0f, 0.0f, 0.0f, 0.0f}, s2 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      s1 = mfma16(k_operand_q<QT, KT>(r0.k1, c), qop[c], s1);
-      s2 = mfma16(k_operand_q<QT, KT>(r0.k2, c), qop[c], s2);
+      if constexpr (QS == 3) {
+        // smallest term first
+        const QOp<QT> ka = k_operand_q<QT, KT>(r0.k1, c), kb = k_operand_q<QT, KT>(r0.k2, c);
+        s1 = mfma16(ka, qop[2 * NC + c], s1);
+        s2 = mfma16(kb, qop[2 * NC + c], s2);
+        s1 = mfma16(ka, qop[NC + c], s1);
+        s2 = mfma16(kb, qop[NC + c], s2);
+        s1 = mfma16(ka, qop[c], s1);
+        s2 = mfma16(kb, qop[c], s2);
+      } else {
+        s1 = mfma16(k_operand_q<QT, KT>(r0.k1, c), qop[c], s1);
+        s2 = mfma16(k_operand_q<QT, KT>(r0.k2, c), qop[c], s2);
+      }
     }
     // lane (li, lq): s1[v] -> token 8lq + v, s2[v] -> token 8lq + 4 + v, column li
     float sc[8];
@@ -651,19 +721,32 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     // ---- O^T += V^T P^T --------------------------------------------------
     if constexpr (KT == kE4M3 || KT == kF16) {
       // e4m3 V converts exactly to fp16 (fp16 V is used as is); P in fp16
-      // (p <= 256) keeps 11 bits.
+      // (p <= 256) keeps 11 bits -- 22 as P_hi + P_lo for fp32 queries.
       f16x8_t pop;
 #pragma unroll
       for (int v = 0; v < 8; ++v) pop[v] = (_Float16)pr[v];
+      if constexpr (QT == kF32) {
+        f16x8_t plo;
 #pragma unroll
-      for (int t = 0; t < NV; ++t) {
-        f16x8_t vop;
-        if constexpr (KT == kE4M3) vop = e4m3x8_to_f16(vraw[t].x, vraw[t].y);
-        else vop = __builtin_bit_cast(f16x8_t, vraw[t]);
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, o[t], 0, 0, 0);
+        for (int v = 0; v < 8; ++v) plo[v] = (_Float16)(pr[v] - (float)pop[v]);
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+          const f16x8_t vop = e4m3x8_to_f16(vraw[t].x, vraw[t].y);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, plo, o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, o[t], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+          f16x8_t vop;
+          if constexpr (KT == kE4M3) vop = e4m3x8_to_f16(vraw[t].x, vraw[t].y);
+          else vop = __builtin_bit_cast(f16x8_t, vraw[t]);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, o[t], 0, 0, 0);
+        }
       }
     } else {
-      // bf16 V: P = P_hi + P_lo in bf16 (two MFMAs) keeps ~16 bits.
+      // bf16 V: P = P_hi + P_lo in bf16 (two MFMAs) keeps ~16 bits; fp32
+      // queries add a third term (24 bits).
       bf16x8_t pop, plo;
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
@@ -671,11 +754,24 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
         pop[v] = hi;
         plo[v] = (__bf16)(pr[v] - (float)hi);
       }
+      if constexpr (QT == kF32) {
+        bf16x8_t pl2;
 #pragma unroll
-      for (int t = 0; t < NV; ++t) {
-        const bf16x8_t vop = as_bf16x8(vraw[t]);
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, o[t], 0, 0, 0);
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo, o[t], 0, 0, 0);
+        for (int v = 0; v < 8; ++v) pl2[v] = (__bf16)((pr[v] - (float)pop[v]) - (float)plo[v]);
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+          const bf16x8_t vop = as_bf16x8(vraw[t]);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pl2, o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo, o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, o[t], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+          const bf16x8_t vop = as_bf16x8(vraw[t]);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo, o[t], 0, 0, 0);
+        }
       }
     }
 
@@ -691,8 +787,12 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(DecodeParams p, cons
     has1 = has2;
     r0 = r1;
     if (run_ends) {
+      if constexpr (QT == kF32) {
+        load_q<QT, D>(qop, p, c0, li, lq);
+      } else {
 #pragma unroll
-      for (int cc = 0; cc < NC; ++cc) qop[cc] = qnext[cc];
+        for (int cc = 0; cc < NC; ++cc) qop[cc] = qnext[cc];
+      }
       m = -INFINITY;
       l = 0.0f;
 #pragma unroll
@@ -771,7 +871,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
         }
       }
     }
-    uint16_t* out = (uint16_t*)p.out + (int64_t)b * p.o_sb;
+    const int64_t out = (int64_t)b * p.o_sb;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       const int idx = lane + 64 * i;
@@ -791,7 +891,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
           a += w * ov[k][i];
         }
       }
-      out[(int64_t)(h * G + g) * p.o_sh + d] = out_bits<QT>(lg > 0.0f ? a / lg : 0.0f);
+      store_out1<QT>(p.out, out + (int64_t)(h * G + g) * p.o_sh + d, lg > 0.0f ? a / lg : 0.0f);
     }
     return;
   }
@@ -913,16 +1013,14 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
       acc[0].w += r.w;
     }
   }
-  uint16_t* out = (uint16_t*)p.out + (int64_t)b * p.o_sb;
+  const int64_t out = (int64_t)b * p.o_sb;
 #pragma unroll
   for (int j = 0; j < FPT; ++j) {
     const int g = gs[j], d = 4 * fs[j] % D;
     const float lg = run_l[g];
-    auto nrm = [&](float a) { return out_bits<QT>(lg > 0.0f ? a / lg : 0.0f); };
-    uint2 packed;
-    packed.x = (uint32_t)nrm(acc[j].x) | ((uint32_t)nrm(acc[j].y) << 16);
-    packed.y = (uint32_t)nrm(acc[j].z) | ((uint32_t)nrm(acc[j].w) << 16);
-    *(uint2*)(out + (int64_t)(h * G + g) * p.o_sh + d) = packed;
+    auto nrm = [&](float a) { return lg > 0.0f ? a / lg : 0.0f; };
+    store_out4<QT>(p.out, out + (int64_t)(h * G + g) * p.o_sh + d, nrm(acc[j].x), nrm(acc[j].y), nrm(acc[j].z),
+                   nrm(acc[j].w));
   }
 }
 
@@ -1048,8 +1146,9 @@ void decode_mfma_bind_workspace(DecodeParams& p, void* workspace) {
 }
 
 bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
-  // bf16 queries over bf16 or e4m3 caches; fp16 queries over fp16 or e4m3
-  if (q_dt == kBF16) {
+  // bf16 or fp32 queries over bf16 or e4m3 caches; fp16 queries over fp16
+  // or e4m3
+  if (q_dt == kBF16 || q_dt == kF32) {
     if (kv_dt != kBF16 && kv_dt != kE4M3) return false;
   } else if (q_dt == kF16) {
     if (kv_dt != kF16 && kv_dt != kE4M3) return false;
@@ -1077,9 +1176,11 @@ bool decode_mfma_supported(const DecodeParams& p, int q_dt, int kv_dt) {
   if ((p.v_s[0] * kb) % 16 != 0 || (p.v_s[2] * kb) % 16 != 0) return false;
   if (v_native && (p.v_s[3] * kb) % 16 != 0) return false;
   if (!aligned16(p.k) || !aligned16(p.v)) return false;
-  // q rows: 16-byte aligned slices; out rows: 8-byte aligned groups of 4.
-  if (!aligned16(p.q) || (p.q_sb * 2) % 16 != 0 || (p.q_sh * 2) % 16 != 0) return false;
-  if (((uintptr_t)p.out & 7) != 0 || (p.o_sb * 2) % 8 != 0 || (p.o_sh * 2) % 8 != 0) return false;
+  // q rows: 16-byte aligned slices; out rows: aligned groups of 4 (8 bytes
+  // of 16-bit codes, 16 bytes of fp32).
+  const int qb = q_dt == kF32 ? 4 : 2, oal = q_dt == kF32 ? 16 : 8;
+  if (!aligned16(p.q) || (p.q_sb * qb) % 16 != 0 || (p.q_sh * qb) % 16 != 0) return false;
+  if (((uintptr_t)p.out & (oal - 1)) != 0 || (p.o_sb * qb) % oal != 0 || (p.o_sh * qb) % oal != 0) return false;
   return true;
 }
 
@@ -1093,6 +1194,7 @@ int32_t launch_d(const DecodeParams& p, hipStream_t stream) {
 
 int32_t launch_decode_mfma(const DecodeParams& p, int q_dt, int kv_dt, hipStream_t stream) {
   if (q_dt == kF16) return kv_dt == kE4M3 ? launch_d<kF16, kE4M3>(p, stream) : launch_d<kF16, kF16>(p, stream);
+  if (q_dt == kF32) return kv_dt == kE4M3 ? launch_d<kF32, kE4M3>(p, stream) : launch_d<kF32, kBF16>(p, stream);
   return kv_dt == kE4M3 ? launch_d<kBF16, kE4M3>(p, stream) : launch_d<kBF16, kBF16>(p, stream);
 }
 

@@ -129,6 +129,60 @@ def test_fp16_queries_take_the_mfma_path(gpu, hq, hkv, d, kv_dtype):
     assert_close(out.float().cpu().numpy(), ref, torch.float16, f"fp16 q / {kv_dtype}")
 
 
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("hq,hkv,d,layout", [(32, 8, 128, "paired"), (16, 2, 64, "native"),
+                                             (8, 8, 64, "token_major"), (32, 8, 128, "token_major")])
+def test_fp32_queries_take_the_mfma_path(gpu, hq, hkv, d, layout, kv_dtype):
+    """fp32 queries over bf16 or e4m3 caches run the MFMA kernel: each query
+    channel split exactly into three bf16 terms, P carried as two fp16 (e4m3
+    V) or three bf16 (bf16 V) terms.  fp32 output within the fp32 bound
+    (max-abs 1e-5) of the float64 oracle, with the shared-prefix statement
+    and a sequence long enough to be split over several waves."""
+    print(f"[case] fp32 q hq={hq} hkv={hkv} d={d} kv={kv_dtype} layout={layout}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(7 * hq + d)
+    lens = [700, 1024, 1024 + 33, 40, 6000, 1, 0, 300]
+    nb = 1000
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(4)).tolist()
+    shared = perm[:64]  # sequences 1 and 2 share a 1024-token prefix
+    tables, pos = [], 64
+    for i, n in enumerate(lens):
+        k = max(1, (n + 15) // 16)
+        if i in (1, 2):
+            own = perm[pos:pos + k - 64]
+            pos += k - 64
+            tables.append(shared + own)
+        else:
+            tables.append(perm[pos:pos + k])
+            pos += k
+    q = torch.randn(len(lens), hq, d, generator=g, device=gpu) * 2.0
+    ksrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
+    vsrc = torch.randn(nb, 16, hkv, d, generator=g, device=gpu).to(torch.bfloat16)
+    case = workloads.DecodeCase("fp32q", q, ksrc, vsrc, tables, lens, 16, 1 / math.sqrt(d), kv_dtype)
+    kc, vc, ks, vs = workloads.materialize(case, layout)
+    sh = torch.tensor(ops.shared_prefix_lens(tables, lens, 16), dtype=torch.int32, device=gpu)
+    ref = oracle_decode(case, kc, vc, ks, vs)
+    with ops.KernelTimer() as timer:
+        out = paged_attention_tensors(q, kc, vc, case.tables_tensor(gpu), case.seq_lens_tensor(gpu), 16, case.scale,
+                                      k_scale=ks, v_scale=vs, shared_prefix_lens=sh)
+        torch.cuda.synchronize()
+        assert timer.query("cf_decode_mfma")[1] == 1 and timer.query("cf_decode_generic")[1] == 0
+    assert out.dtype == torch.float32
+    assert_close(out.cpu().numpy(), ref, torch.float32, f"fp32 q / {kv_dtype} / {layout}")
+
+
+def test_fp32_queries_c3_batch(gpu):
+    """The c3 workload (e4m3 with 1 % x8 outliers, per-head scales, shared
+    prefix) at batch 8 with fp32 queries: MFMA path, fp32 bound."""
+    case = workloads.make_case("c3_llama3_8b", device=gpu, seed=12, batch=8)
+    case.q = case.q.float()
+    kc, vc, ks, vs = workloads.materialize(case, "paired")
+    sh = torch.tensor(ops.shared_prefix_lens(case.block_tables, case.seq_lens, 16), dtype=torch.int32, device=gpu)
+    out = paged_attention_tensors(case.q, kc, vc, case.tables_tensor(gpu), case.seq_lens_tensor(gpu), 16, case.scale,
+                                  k_scale=ks, v_scale=vs, shared_prefix_lens=sh)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), oracle_decode(case, kc, vc, ks, vs), torch.float32, "c3 fp32 q")
+
+
 def test_edge_lengths(gpu):
     """Zero length -> zeros; length past the table -> truncated to it."""
     case = workloads.make_case("c2_tinyllama", device=gpu, seed=4, batch=4)
