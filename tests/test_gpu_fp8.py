@@ -54,6 +54,29 @@ def test_quantize_with_a_scale_exhaustive(gpu):
     assert bad == 0
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_quantize_near_midpoints_many_scales(gpu, seed):
+    """Inputs within 24 ulp of x = M * s for every midpoint M between adjacent
+    e4m3 codes (subnormal codes, normal codes, and 464 between 448 and the
+    NaN code), both signs, at 64 random scales: the inputs where x * (1/s)
+    and x / s may encode differently, which the encoder resolves without a
+    division in the normal range."""
+    rng = np.random.default_rng(100 + seed)
+    vals = ofp8.decode(np.arange(0x00, 0x7F, dtype=np.uint8)).astype(np.float64)  # 0 .. 448
+    mids = np.concatenate([(vals[:-1] + vals[1:]) / 2, [464.0]])
+    ks = np.arange(-24, 25, dtype=np.int64)
+    for s in (rng.uniform(0.5, 2.0, 64) * 2.0 ** rng.integers(-40, 40, 64)).astype(np.float32):
+        x0 = (mids * np.float64(s)).astype(np.float32)
+        bits = x0.view(np.uint32).astype(np.int64)[:, None] + ks[None, :]
+        x = bits.astype(np.uint32).view(np.float32).reshape(-1)
+        x = np.concatenate([x, -x])
+        got = ops.fp8_quantize(torch.from_numpy(x).to(gpu).view(1, 1, -1),
+                               torch.full((1,), float(s), dtype=torch.float32, device=gpu))
+        got = got.view(torch.uint8).view(-1).cpu().numpy()
+        want = ofp8.quantize(x, s)
+        assert np.array_equal(got, want), (float(s), int(np.count_nonzero(got != want)))
+
+
 @pytest.mark.parametrize("s", [3.0, 1.0 / 3.0, 1.234e-5, 7.77e3, 1e-12, 1e-39, 3e38])
 def test_quantize_scales_on_random_patterns(gpu, s):
     """2^26 random float32 patterns (every exponent, NaN and inf included)
