@@ -190,11 +190,13 @@ def _e4m3_rows(ic: PagedKVIntercept, slab: str, layer: int, table: list[int], n:
     return vals[np.asarray(table)[tok // 16], tok % 16]
 
 
-def test_llama_shaped_prefill_then_decode_from_fp8_slabs(gpu):
-    """Llama-3-8B attention shape, e4m3 slabs, bf16 activations, one request:
-    a 300-token chunk at 0..299, a second chunk at 300..599 (sees the cached
-    prefix), then a decode at 600 -- every output from the slabs, against the
-    float64 oracle on the codes the slabs hold."""
+@pytest.mark.parametrize("act", [torch.bfloat16, torch.float16])
+def test_llama_shaped_prefill_then_decode_from_fp8_slabs(gpu, act):
+    """Llama-3-8B attention shape, e4m3 slabs, bf16 or fp16 activations, one
+    request: a 300-token chunk at 0..299, a second chunk at 300..599 (sees
+    the cached prefix), then a decode at 600 -- every output from the slabs
+    on the HIP kernels (no dense fallback), against the float64 oracle on the
+    codes the slabs hold."""
     hq, hkv, d, layers = 32, 8, 128, 2
     ic = PagedKVIntercept.from_module(_module(layers, heads=hkv, dim=d, dtype="float8_e4m3fn"), device=gpu,
                                       prefill_from_slabs=True)
@@ -206,13 +208,13 @@ def test_llama_shaped_prefill_then_decode_from_fp8_slabs(gpu):
     hal = _DenseSdpa()
     layer = 1  # the second layer's op (the first consumes layer 0's counters)
     for start, n, decode in ((0, 300, False), (300, 300, False), (600, 1, True)):
-        print(f"[case] intercept llama chunk start={start} rows={n} decode={decode}", flush=True)
+        print(f"[case] intercept llama {act} chunk start={start} rows={n} decode={decode}", flush=True)
         ic.begin_step(tables, positions=torch.arange(start, start + n), is_decode=decode)
-        q = torch.randn(1, hq, n, d, generator=g, device=gpu).to(torch.bfloat16)
+        q = torch.randn(1, hq, n, d, generator=g, device=gpu).to(act)
         results = []
         for lay in range(layers):
-            k = torch.randn(1, hkv, n, d, generator=g, device=gpu).to(torch.bfloat16)
-            v = torch.randn(1, hkv, n, d, generator=g, device=gpu).to(torch.bfloat16)
+            k = torch.randn(1, hkv, n, d, generator=g, device=gpu).to(act)
+            v = torch.randn(1, hkv, n, d, generator=g, device=gpu).to(act)
             ssa = {f"%k{lay}": k, f"%v{lay}": v}
             ic.handle(_sdpa_op(lay), ssa)
             assert ssa[f"%k{lay}"] is k  # never substituted
@@ -221,7 +223,7 @@ def test_llama_shaped_prefill_then_decode_from_fp8_slabs(gpu):
         torch.cuda.synchronize()
         assert hal.calls == 0
         out = results[layer]
-        assert out.shape == (1, hq, n, d) and out.dtype == torch.bfloat16
+        assert out.shape == (1, hq, n, d) and out.dtype == act
         kk = _e4m3_rows(ic, "k", layer, table, start + n)
         vv = _e4m3_rows(ic, "v", layer, table, start + n)
         kc, vc = kk[:, None], vv[:, None]  # one-token blocks
@@ -229,7 +231,7 @@ def test_llama_shaped_prefill_then_decode_from_fp8_slabs(gpu):
         ref, _ = paged_prefill_fp64(qrows, kc, vc, [list(range(start + n))], [start + n], [0, n], 1,
                                     1 / math.sqrt(d))
         got = out[0].permute(1, 0, 2).float().cpu().numpy()
-        assert_close(got, ref, torch.bfloat16, f"intercept llama start={start} n={n}")
+        assert_close(got, ref, act, f"intercept llama {act} start={start} n={n}")
 
 
 def test_default_prefill_is_the_reference_dense_sdpa(gpu):
